@@ -1,0 +1,328 @@
+#!/usr/bin/env python3
+"""Benchmark of the WUSH INT4 W4A4 layer on one MI355X.
+
+Metric: microseconds per layer, and speedup vs hipBLASLt
+bf16, for the Llama-70B FFN shape K=8192, N=57344 at M = 1 / 8 / 32 / 4096.
+
+A "step" is one forward pass of the layer's hot path over one batch of
+synthetic activations, exactly as the reference's official bench chains it
+(reference bench/exp_p13_official.py:31-39):
+  M <= 8 : fused transform+quant -> w4a4_gemv / w4a4_gemv_multi
+  M >  8 : fused transform+quant -> w4a4_gemm_s4
+with the weights pre-quantized (W' = W T^-1, sigma-clip s4 + bf16 scales) and
+resident in HBM.  Each chain is captured in a HIP graph and replayed
+round-robin over several distinct weight copies (> the 256 MB MALL), so every
+step streams the weights from HBM.  `value` is the M=1 layer time (the
+headline decode point); the other M are reported beside it, each with the
+hipBLASLt bf16 GEMM time at the same shape measured the same way.
+
+Also reported: the roofline of the dominant kernel at M=1 (gemv_int4, HBM-
+bound; timed alone with HIP events on its launch stream), and the CPU
+baseline -- the project's CPU restatement of the reference path (oracle/:
+rtn quant of x + dequantized fp32 matmul), timed on a bounded sample on this
+host with 1 thread and scaled to the full layer.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "µs/layer + speedup vs hipBLASLt bf16, K=8192 N=57344 at M=1/8/32/4096"
+K_L70, N_L70 = 8192, 57344
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_int4_l70_m1_traffic.txt")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--ms", default="1,8,32,4096", help="comma-separated M values")
+    ap.add_argument("--copies", type=int, default=3, help="distinct weight copies (MALL defeat)")
+    ap.add_argument("--no-blas", action="store_true", help="skip the hipBLASLt bf16 baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--K", type=int, default=K_L70)
+    ap.add_argument("--N", type=int, default=N_L70)
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only launch the M=1 dominant kernel (for rocprofv3 runs)")
+    return ap.parse_args()
+
+
+def layer_bytes(M, N, K):
+    """Algorithmic HBM bytes of one layer: x bf16 + T bf16 + W4 codes/scales + y fp16."""
+    return 2 * M * K + 64 * K + N * K // 2 + N * K // 16 + 2 * M * N
+
+
+def gemv_bytes(M, N, K):
+    """Algorithmic bytes of one gemv_int4 launch: x codes/scales, W4 codes/scales, y fp16."""
+    return M * K // 2 + M * K // 16 + N * K // 2 + N * K // 16 + 2 * M * N
+
+
+def read_traffic():
+    """HBM bytes per launch of gemv_int4 at L70 M=1 from the committed rocprofv3 summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the W4A4 layer path has no "
+                          "multi-GPU mode (see DESIGN.md for how it would shard along N); "
+                          "run with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+    from my_int4 import _C
+    from wush_int4_kernel_amd import capi
+    from wush_int4_kernel_amd.wush_transform import compute_wush_transform, transform_weights
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    K, N = args.K, args.N
+    Ms = [int(m) for m in args.ms.split(",") if m]
+
+    # ---------------------------------------------------------------- inputs
+    t0 = time.time()
+    gcpu = torch.Generator().manual_seed(0)
+    n_out = int(round(0.01 * K))
+    out_ch = torch.randperm(K, generator=gcpu)[:n_out].to(dev)
+    gdev = torch.Generator(device=dev).manual_seed(0)
+
+    def activations(M, gen):
+        x = torch.randn(M, K, generator=gen, device=dev, dtype=torch.float32)
+        x[:, out_ch] *= 50.0
+        return x
+
+    W = torch.randn(N, K, generator=gdev, device=dev, dtype=torch.float32) * 0.02
+    Xcal = activations(512, gdev)
+    T64 = compute_wush_transform(Xcal.double(), W.double())
+    T = T64.to(torch.bfloat16).contiguous()
+    Wt = transform_weights(W.double(), T64).to(torch.bfloat16).contiguous()
+    wq, ws = _C.quant_int4(Wt)
+    del W, Xcal
+    torch.cuda.synchronize()
+    copies = [(wq, ws)] + [(wq.clone(), ws.clone()) for _ in range(args.copies - 1)]
+    log(f"[bench] weights ready: N={N} K={K}, {args.copies} copies x "
+        f"{(wq.numel() + ws.numel() * 2) / 1e6:.1f} MB ({time.time() - t0:.1f}s)")
+
+    stream = torch.cuda.current_stream()
+
+    def chain_fn(X, wq_, ws_, M):
+        if M == 1:
+            return lambda: _C.w4a4_gemv(*_C.fused_transform_quant_int4_smallm(X, T), wq_, ws_)
+        if M <= 8:
+            return lambda: _C.w4a4_gemv_multi(*_C.fused_transform_quant_int4_smallm(X, T), wq_, ws_)
+        return lambda: _C.w4a4_gemm_s4(*_C.fused_transform_quant_int4_v3(X, T), wq_, ws_)
+
+    def capture(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        return g
+
+    def time_graphs(graphs, steps, warmup):
+        for i in range(warmup):
+            graphs[i % len(graphs)].replay()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for i in range(steps):
+            graphs[i % len(graphs)].replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) / steps
+
+    # -------------------------------------------------------- kernel-only mode
+    if args.kernel_only:
+        M = 1
+        X = activations(M, gdev).to(torch.bfloat16)
+        xq, xs = _C.fused_transform_quant_int4_smallm(X, T)
+        y = torch.empty(M, N, dtype=torch.float16, device=dev)
+        for i in range(args.warmup + args.steps):
+            cq, cs = copies[i % len(copies)]
+            capi.gemv_int4(xq.data_ptr(), xs.data_ptr(), cq.data_ptr(), cs.data_ptr(), y.data_ptr(),
+                           M, N, K, stream.cuda_stream)
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": "gemv_int4", "launches": args.warmup + args.steps}))
+        return
+
+    # ------------------------------------------------------------- layer sweep
+    layers = {}
+    blas_w = None
+    for M in Ms:
+        X = activations(M, gdev).to(torch.bfloat16).contiguous()
+        graphs = [capture(chain_fn(X, cq, cs, M)) for cq, cs in copies]
+        steps = args.steps if M <= 64 else max(10, args.steps // 10)
+        warm = args.warmup if M <= 64 else max(3, args.warmup // 4)
+        t_int4 = time_graphs(graphs, steps, warm)
+        del graphs
+        entry = {
+            "us": round(t_int4 * 1e6, 2),
+            "chain": ("fused_tq(smallm)+gemv" if M <= 8 else "fused_tq+gemm_s4"),
+            "layer_bytes": layer_bytes(M, N, K),
+            "hbm_gbs": round(layer_bytes(M, N, K) / t_int4 / 1e9, 1),
+            "hbm_frac": round(layer_bytes(M, N, K) / t_int4 / 1e9 / HBM_PEAK_GBS, 4),
+            "int8_tops": round(2 * M * N * K / t_int4 / 1e12, 2),
+            "int8_mfma_frac": round(2 * M * N * K / t_int4 / 1e12 / INT8_PEAK_TOPS, 4),
+        }
+        if not args.no_blas:
+            torch.backends.cuda.preferred_blas_library("hipblaslt")
+            if blas_w is None:
+                blas_w = [Wt] + [Wt.clone() for _ in range(1)]
+            Xb = X
+            bgraphs = []
+            for Wc in blas_w:
+                bgraphs.append(capture(lambda Wc=Wc: torch.matmul(Xb, Wc.t())))
+            t_blas = time_graphs(bgraphs, steps, warm)
+            del bgraphs
+            entry["hipblaslt_bf16_us"] = round(t_blas * 1e6, 2)
+            entry["speedup_vs_hipblaslt"] = round(t_blas / t_int4, 3)
+        layers[f"M={M}"] = entry
+        log(f"[bench] M={M}: {entry}")
+
+    # --------------------------------------------- roofline of the M=1 kernel
+    M = 1
+    X = activations(M, gdev).to(torch.bfloat16)
+    xq, xs = _C.fused_transform_quant_int4_smallm(X, T)
+    y = torch.empty(M, N, dtype=torch.float16, device=dev)
+    launches = max(50, args.steps)
+
+    def launch(i):
+        cq, cs = copies[i % len(copies)]
+        capi.gemv_int4(xq.data_ptr(), xs.data_ptr(), cq.data_ptr(), cs.data_ptr(), y.data_ptr(),
+                       M, N, K, stream.cuda_stream)
+
+    for i in range(10):
+        launch(i)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(launches):
+        launch(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t_kernel = e0.elapsed_time(e1) / 1e3 / launches
+    alg = gemv_bytes(M, N, K)
+    achieved = alg / t_kernel / 1e9
+    roofline = {
+        "kernel": "gemv_int4_kernel<1> (L70, M=1)",
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": read_traffic(),
+        "algorithmic_bytes": alg,
+        "avg_launch_us": round(t_kernel * 1e6, 2),
+    }
+    log(f"[bench] roofline: {roofline}")
+
+    # ------------------------------------------------------------ CPU baseline
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(wq, ws, X, N, K)
+        log(f"[bench] cpu baseline: {cpu}")
+
+    head = layers.get("M=1") or next(iter(layers.values()))
+    out = {
+        "metric": METRIC,
+        "value": head["us"],
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us"] / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4",
+        "data": "synthetic: seeded N(0,1) activations with 1% outlier channels x50, N(0,0.02) weights "
+                "transformed by this build's WUSH T and sigma-clip quantized",
+        "config": {
+            "workload": f"Llama-70B FFN layer K={K} N={N}, M=1: fused_tq(smallm) + gemv_int4, "
+                        f"HIP graph, {args.copies} weight copies rotated",
+            "K": K, "N": N, "M": 1,
+        },
+        "layers": layers,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "device": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(out))
+
+
+def cpu_baseline(wq, ws, X, N, K):
+    """The reference CPU path on this host: rtn quant of x + dequant of W +
+    fp32 matmul (my_int4/rtn_int4.py:33-75), via the oracle (C, 1 thread) and
+    torch CPU matmul pinned to 1 thread; a 4096-row weight sample, median of
+    5, scaled to the full N."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    torch.set_num_threads(1)
+    S = min(4096, N)
+    wq_s = wq[:S].cpu().numpy()
+    ws_s = ws[:S].cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+    xb = X.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    def med(fn, reps=5):
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return statistics.median(ts)
+
+    oracle.quant(xb, "bf16")
+    t_qx = med(lambda: oracle.quant(xb, "bf16"))
+    xq, xs = oracle.quant(xb, "bf16")
+    xd = torch.from_numpy(oracle.dequant(xq, xs))
+    t_dw = med(lambda: oracle.dequant(wq_s, ws_s))
+    wd = torch.from_numpy(oracle.dequant(wq_s, ws_s))
+    t_mm = med(lambda: xd @ wd.T)
+    per_layer = t_qx + (t_dw + t_mm) * (N / S)
+    try:
+        cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except Exception:
+        cpu_model = platform.processor()
+    return {
+        "value": round(per_layer * 1e6, 1),
+        "unit": "us/layer",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"L70 layer M=1: quant(x 1x{K}) + dequant(W {S}x{K} of {N} rows) + fp32 matmul, "
+                  f"median of 5, scaled by N/{S}; quant {t_qx * 1e6:.0f} us, dequant {t_dw * 1e3:.1f} ms, "
+                  f"matmul {t_mm * 1e3:.2f} ms per sample",
+        "host": {"cpu_model": cpu_model, "os_cpu_count": os.cpu_count(), "torch_threads": 1},
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,353 @@
+"""GPU parity tests through the C ABI (include/wush_int4.h via ctypes).
+
+torch supplies device memory and the stream only.  Bars:
+  * quant_int4 / fused_tq: codes and bf16 scale bits bit-exact vs the oracle
+    and the committed fixtures;
+  * GEMV / GEMM: the int32 group dots exact (unit scales, |Y| < 2048 so fp16
+    holds them exactly) and the fp16 output within 2e-3 relative Frobenius of
+    the fp64 dequantized product (the tolerance the north star states);
+  * MFMA layout self-test exact.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from _util import (bf16_bits_to_f32, f16_tensor_f64, f32_to_bf16_bits, outlier_activations,
+                   pack_codes, rel_fro, rng, to_dev_bf16, to_dev_u8, unpack_codes)
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+FRO_TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def capi():
+    import torch  # noqa: F401  (HIP runtime first)
+    from wush_int4_kernel_amd import capi as c
+    c.load()
+    return c
+
+
+def _stream():
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _bits(t) -> np.ndarray:
+    import torch
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def run_quant(capi, x_np: np.ndarray, dtype: str):
+    import torch
+    if dtype == "bf16":
+        xt = to_dev_bf16(x_np)
+        code = capi.DTYPE_BF16
+    elif dtype == "f16":
+        xt = torch.from_numpy(np.ascontiguousarray(x_np, dtype=np.float16)).cuda()
+        code = capi.DTYPE_F16
+    else:
+        xt = torch.from_numpy(np.ascontiguousarray(x_np, dtype=np.float32)).cuda()
+        code = capi.DTYPE_F32
+    n_groups = xt.numel() // 32
+    q = torch.empty(xt.numel() // 2, dtype=torch.uint8, device="cuda")
+    s = torch.empty(n_groups, dtype=torch.bfloat16, device="cuda")
+    capi.quant_int4(xt.data_ptr(), code, q.data_ptr(), s.data_ptr(), n_groups, _stream())
+    torch.cuda.synchronize()
+    K = x_np.shape[-1]
+    return q.cpu().numpy().reshape(x_np.shape[:-1] + (K // 2,)), _bits(s).reshape(x_np.shape[:-1] + (K // 32,))
+
+
+def run_fused(capi, xb: np.ndarray, tb: np.ndarray):
+    import torch
+    xt = to_dev_bf16(xb)
+    tt = to_dev_bf16(tb)
+    K = xb.shape[-1]
+    rows = xb.size // K
+    q = torch.empty(rows * K // 2, dtype=torch.uint8, device="cuda")
+    s = torch.empty(rows * K // 32, dtype=torch.bfloat16, device="cuda")
+    capi.fused_tq(xt.data_ptr(), tt.data_ptr(), q.data_ptr(), s.data_ptr(), rows, K, _stream())
+    torch.cuda.synchronize()
+    return q.cpu().numpy().reshape(xb.shape[:-1] + (K // 2,)), _bits(s).reshape(xb.shape[:-1] + (K // 32,))
+
+
+def _dev_operands(xq, xs, wq, ws):
+    return to_dev_u8(xq), to_dev_bf16(xs), to_dev_u8(wq), to_dev_bf16(ws)
+
+
+def run_gemm(capi, xq, xs, wq, ws, kernel="gemm"):
+    import torch
+    M, K2 = xq.shape
+    N = wq.shape[0]
+    K = 2 * K2
+    dx, dxs, dw, dws = _dev_operands(xq, xs, wq, ws)
+    y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    if kernel == "gemv":
+        capi.gemv_int4(dx.data_ptr(), dxs.data_ptr(), dw.data_ptr(), dws.data_ptr(), y.data_ptr(),
+                       M, N, K, _stream())
+    else:
+        wsb = capi.gemm_s4_workspace_bytes(M, N, K)
+        work = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+        capi.gemm_s4(dx.data_ptr(), dxs.data_ptr(), dw.data_ptr(), dws.data_ptr(), y.data_ptr(),
+                     M, N, K, work.data_ptr() if wsb else None, wsb, _stream())
+    torch.cuda.synchronize()
+    return f16_tensor_f64(y)
+
+
+# --------------------------------------------------------------------- quant
+def test_quant_golden_fixture(capi):
+    kat = np.load(os.path.join(GOLDEN, "quant_kat.npz"))
+    q, s = run_quant(capi, kat["x_bf16"], "bf16")
+    assert np.array_equal(q, kat["q"]) and np.array_equal(s, kat["s"])
+
+
+@pytest.mark.parametrize("shape", [(4096, 32), (2, 3, 96), (1, 32), (7, 4096), (1 << 17, 128)])
+def test_quant_bf16_random(capi, shape):
+    g = rng(1000 + len(shape) * 7 + shape[-1])
+    x = f32_to_bf16_bits(g.standard_normal(shape).astype(np.float32))
+    q, s = run_quant(capi, x, "bf16")
+    qo, so = oracle.quant(x, "bf16")
+    assert np.array_equal(q, qo), np.argwhere(q != qo)[:5]
+    assert np.array_equal(s, so)
+
+
+def test_quant_outliers_zeros_ties_overflow(capi):
+    g = rng(1001)
+    blocks = [outlier_activations(g, 64, 4096).reshape(-1, 32)]
+    blocks.append(np.zeros((4, 32), np.uint16))
+    t = np.zeros((2, 32), np.float32)
+    t[0, :8] = [7.0, -7.0, 2.5, -2.5, 3.5, -3.5, 0.5, -0.5]
+    t[1, :8] = np.array([0.5, 1.5, 2.5, 3.5, 4.5, 5.5, 6.5, -6.5], np.float32) * np.float32(0.7)
+    blocks.append(f32_to_bf16_bits(t))
+    blocks.append(f32_to_bf16_bits(np.full((4, 32), 3.3e38, np.float32)))
+    special = np.zeros((3, 32), np.float32)
+    special[0, 3] = np.inf
+    special[1, 4] = -np.inf
+    special[1, 9] = 2.0
+    special[2, :] = g.standard_normal(32)
+    special[2, 7] = np.nan
+    blocks.append(f32_to_bf16_bits(special))
+    blocks.append(f32_to_bf16_bits((g.standard_normal((64, 32)) * 1e-39).astype(np.float32)))  # subnormal
+    x = np.concatenate(blocks, axis=0)
+    q, s = run_quant(capi, x, "bf16")
+    qo, so = oracle.quant(x, "bf16")
+    assert np.array_equal(q, qo) and np.array_equal(s, so)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_quant_other_dtypes(capi, dtype):
+    g = rng(1002)
+    x = bf16_bits_to_f32(outlier_activations(g, 16, 4096))
+    if dtype == "f16":
+        x = x.astype(np.float16)
+        q, s = run_quant(capi, x, "f16")
+        qo, so = oracle.quant(x.view(np.uint16), "f16")
+    else:
+        x = x * np.float32(1.0001)          # values that are not bf16-representable
+        q, s = run_quant(capi, x, "f32")
+        qo, so = oracle.quant(x, "f32")
+    assert np.array_equal(q, qo) and np.array_equal(s, so)
+
+
+# --------------------------------------------------------------------- fused
+def test_fused_golden_fixture(capi):
+    fz = np.load(os.path.join(GOLDEN, "fused_small.npz"))
+    q, s = run_fused(capi, fz["x_bf16"], fz["t_bf16"])
+    assert np.array_equal(q, fz["q"]) and np.array_equal(s, fz["s"])
+
+
+@pytest.mark.parametrize("rows,K", [(1, 32), (1, 4096), (3, 96), (8, 8192), (63, 256), (64, 256),
+                                    (65, 512), (130, 128), (256, 4096), (1 << 16, 64)])
+def test_fused_random(capi, rows, K):
+    g = rng(2000 + rows + K)
+    xb = outlier_activations(g, rows, K)
+    tb = f32_to_bf16_bits(g.standard_normal((K // 32, 32, 32)) * 0.25)
+    q, s = run_fused(capi, xb, tb)
+    qo, so = oracle.fused_tq(xb, tb)
+    assert np.array_equal(q, qo), (rows, K, np.argwhere(q != qo)[:5])
+    assert np.array_equal(s, so)
+
+
+def test_fused_permutation_identity_zeros(capi):
+    g = rng(2001)
+    K = 128
+    xb = outlier_activations(g, 70, K)
+    T = np.zeros((K // 32, 32, 32), np.float32)
+    for c in range(K // 32):
+        T[c, np.arange(32), g.permutation(32)] = 1.0
+    for tb in (f32_to_bf16_bits(T), f32_to_bf16_bits(np.broadcast_to(np.eye(32), T.shape))):
+        for rows in (5, 70):
+            q, s = run_fused(capi, xb[:rows], tb)
+            qo, so = oracle.fused_tq(xb[:rows], tb)
+            assert np.array_equal(q, qo) and np.array_equal(s, so)
+    z = np.zeros((4, 64), np.uint16)
+    q, s = run_fused(capi, z, f32_to_bf16_bits(g.standard_normal((2, 32, 32))))
+    assert (q == 0).all() and (s == 0x322C).all()
+
+
+def test_fused_3d_shape(capi):
+    g = rng(2002)
+    xb = f32_to_bf16_bits(g.standard_normal((2, 3, 96)))
+    tb = f32_to_bf16_bits(g.standard_normal((3, 32, 32)))
+    q, s = run_fused(capi, xb, tb)
+    qo, so = oracle.fused_tq(xb, tb)
+    assert q.shape == (2, 3, 48) and s.shape == (2, 3, 3)
+    assert np.array_equal(q, qo) and np.array_equal(s, so)
+
+
+# ----------------------------------------------------------------- GEMV/GEMM
+def _rand_operands(g, M, N, K):
+    xq, xs = oracle.quant(outlier_activations(g, M, K), "bf16")
+    wq, ws = oracle.quant(f32_to_bf16_bits(g.standard_normal((N, K)) * 0.02), "bf16")
+    return xq, xs, wq, ws
+
+
+def _unit_scale_operands(g, M, N, K):
+    # codes bounded so that |Y| = |sum qx*qw| < 2048 is exact in fp16
+    lim = max(1, int(np.sqrt(2000.0 / K)))
+    cx = g.integers(-lim, lim + 1, (M, K))
+    cw = g.integers(-7, 8, (N, K)) if lim * 7 * K < 2048 else g.integers(-lim, lim + 1, (N, K))
+    xs = np.full((M, K // 32), 0x3F80, np.uint16)
+    ws = np.full((N, K // 32), 0x3F80, np.uint16)
+    return pack_codes(cx), xs, pack_codes(cw), ws, (cx @ cw.T).astype(np.float64)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_gemv_matches_oracle(capi, M):
+    g = rng(3000 + M)
+    for N, K in [(64, 64), (300, 512), (4096, 4096)]:
+        xq, xs, wq, ws = _rand_operands(g, M, N, K)
+        y = run_gemm(capi, xq, xs, wq, ws, "gemv")
+        ref = oracle.gemm_f64(xq, xs, wq, ws)
+        assert rel_fro(y, ref) < FRO_TOL, (M, N, K, rel_fro(y, ref))
+
+
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_gemv_int_exact(capi, M):
+    g = rng(3100 + M)
+    xq, xs, wq, ws, yi = _unit_scale_operands(g, M, 200, 256)
+    y = run_gemm(capi, xq, xs, wq, ws, "gemv")
+    assert np.array_equal(y, yi)
+
+
+# shapes of the reference's fp64 arbitration (tests/test_p13.py:18) plus edges
+GEMM_SHAPES = [(64, 96, 128), (1, 64, 64), (300, 500, 512), (130, 512, 4096), (8, 4096, 4096),
+               (33, 200, 96), (257, 33, 96), (8, 32, 32), (32, 1000, 1024), (200, 130, 2048)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_gemm_matches_oracle(capi, M, N, K):
+    g = rng(4000 + M * 7 + N + K)
+    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    y = run_gemm(capi, xq, xs, wq, ws)
+    ref = oracle.gemm_f64(xq, xs, wq, ws)
+    assert rel_fro(y, ref) < FRO_TOL, (M, N, K, rel_fro(y, ref))
+    # the reference gate (tests/test_p13.py:23-27) holds too
+    assert np.abs(y - ref).max() < 0.05 * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 64), (8, 300, 256), (40, 130, 128), (150, 260, 96)])
+def test_gemm_int_exact(capi, M, N, K):
+    g = rng(4100 + M + N + K)
+    xq, xs, wq, ws, yi = _unit_scale_operands(g, M, N, K)
+    y = run_gemm(capi, xq, xs, wq, ws)
+    assert np.array_equal(y, yi)
+
+
+def test_gemm_group_dots_exact_per_group(capi):
+    # One group at a time: scales 1 on group g only, 0 elsewhere -> y = D[:, :, g].
+    g = rng(4200)
+    M, N, K = 16, 96, 128
+    xq, _, wq, _ = _rand_operands(g, M, N, K)
+    D = oracle.group_dots(xq, wq)
+    for gg in range(K // 32):
+        xs = np.zeros((M, K // 32), np.uint16)
+        ws = np.zeros((N, K // 32), np.uint16)
+        xs[:, gg] = 0x3F80
+        ws[:, gg] = 0x3F80
+        for kernel in ("gemm", "gemv"):
+            xs_k = xs[:8] if kernel == "gemv" else xs
+            xq_k = xq[:8] if kernel == "gemv" else xq
+            y = run_gemm(capi, xq_k, xs_k, wq, ws, kernel)
+            assert np.array_equal(y, D[: y.shape[0], :, gg].astype(np.float64)), (kernel, gg)
+
+
+def test_gemm_golden_fixture(capi):
+    gm = np.load(os.path.join(GOLDEN, "gemm_small.npz"))
+    y = run_gemm(capi, gm["xq"], gm["xs"], gm["wq"], gm["ws"])
+    assert rel_fro(y, gm["y_f64"]) < FRO_TOL
+    y = run_gemm(capi, gm["xq"], gm["xs"], gm["wq"], gm["ws"], "gemv")
+    assert rel_fro(y, gm["y_f64"]) < FRO_TOL
+
+
+def test_gemm_zero_activations(capi):
+    g = rng(4300)
+    xq = np.zeros((4, 32), np.uint8)
+    xs = np.full((4, 2), 0x322C, np.uint16)
+    _, _, wq, ws = _rand_operands(g, 1, 16, 64)
+    assert (run_gemm(capi, xq, xs, wq, ws) == 0).all()
+    assert (run_gemm(capi, xq, xs, wq, ws, "gemv") == 0).all()
+
+
+def test_mfma_selftest(capi):
+    import torch
+    g = rng(5000)
+    a = g.integers(-8, 8, (8, 32)).astype(np.int8)
+    b = g.integers(-8, 8, (32, 8)).astype(np.int8)
+    da = torch.from_numpy(a).cuda()
+    db = torch.from_numpy(b).cuda()
+    c = torch.zeros(8, 8, dtype=torch.int32, device="cuda")
+    capi.mfma_selftest(da.data_ptr(), db.data_ptr(), c.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(c.cpu().numpy(), oracle.int_matmul_8x32x8(a, b))
+
+
+# --------------------------------------------------------------- per-tensor
+def test_per_tensor_quant_and_gemm(capi):
+    import torch
+    g = rng(6000)
+    for shape in [(1, 4096), (64, 4096), (2048, 512)]:
+        x = f32_to_bf16_bits(g.standard_normal(shape))
+        amax = float(np.abs(bf16_bits_to_f32(x)).max())
+        inv = np.float32(1.0 / (amax / 7.0))
+        xt = to_dev_bf16(x)
+        q = torch.empty(x.size // 2, dtype=torch.uint8, device="cuda")
+        capi.quant_int4_tensor_scale(xt.data_ptr(), q.data_ptr(), x.size, float(inv), None, _stream())
+        inv_dev = torch.tensor([inv], dtype=torch.float32, device="cuda")
+        q2 = torch.empty_like(q)
+        capi.quant_int4_tensor_scale(xt.data_ptr(), q2.data_ptr(), x.size, 0.0, inv_dev.data_ptr(), _stream())
+        torch.cuda.synchronize()
+        qo = oracle.quant_tensor_scale(x, inv)
+        assert np.array_equal(q.cpu().numpy(), qo) and np.array_equal(q2.cpu().numpy(), qo)
+    for M, N, K in [(64, 96, 128), (1, 256, 64), (300, 500, 512), (8, 4096, 4096)]:
+        xq = pack_codes(g.integers(-7, 8, (M, K)))
+        wq = pack_codes(g.integers(-7, 8, (N, K)))
+        alpha = 1.0 / 64.0
+        dx, dw = to_dev_u8(xq), to_dev_u8(wq)
+        y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+        capi.gemm_s4_tensor_scale(dx.data_ptr(), dw.data_ptr(), y.data_ptr(), M, N, K, alpha, None, _stream())
+        a_dev = torch.tensor([alpha], dtype=torch.float32, device="cuda")
+        y2 = torch.empty_like(y)
+        capi.gemm_s4_tensor_scale(dx.data_ptr(), dw.data_ptr(), y2.data_ptr(), M, N, K, 0.0,
+                                  a_dev.data_ptr(), _stream())
+        torch.cuda.synchronize()
+        ref = oracle.gemm_tensor_scale_f64(xq, wq, alpha)
+        assert rel_fro(f16_tensor_f64(y), ref) < FRO_TOL
+        assert np.array_equal(f16_tensor_f64(y), f16_tensor_f64(y2))
+
+
+def test_invalid_arguments_rejected(capi):
+    import torch
+    x = torch.zeros(64, dtype=torch.bfloat16, device="cuda")
+    q = torch.empty(32, dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        capi.quant_int4(x.data_ptr(), 7, q.data_ptr(), q.data_ptr(), 2, _stream())
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        capi.fused_tq(x.data_ptr(), x.data_ptr(), q.data_ptr(), q.data_ptr(), 1, 48, _stream())
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        capi.gemv_int4(q.data_ptr(), x.data_ptr(), q.data_ptr(), x.data_ptr(), x.data_ptr(), 9, 1, 64, _stream())

@@ -1,0 +1,118 @@
+"""CPU checks of the native artefacts: the C-ABI library loads and exports
+every symbol include/wush_int4.h declares; argument validation rejects bad
+calls before any device work; the torch module exposes the reference's 16 ops
+(reference csrc/bindings.cpp:28-68) and rejects CPU tensors like the
+reference does.  No kernel is launched here (there is no GPU)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "wush_int4.h")
+INVALID = 1  # hipErrorInvalidValue
+
+REFERENCE_OPS = [
+    "quant_int4_tensor_scale", "quant_int4_tensor_scale_dev", "quant_int4", "w4a4_gemm",
+    "w4a4_gemm_v1", "w4a4_gemm_cutlass", "w4a4_gemm_cutlass_dev", "w4a4_gemm_s4",
+    "s4_atom_selftest", "w4a4_gemv", "w4a4_gemv_multi", "fused_transform_quant_int4_v3",
+    "fused_transform_quant_int4_smallm", "fused_transform_quant_int4", "w4a4_gemm_v2",
+    "fused_transform_quant_int4_wmma",
+]
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(wush_[a-z0-9_]+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def capi():
+    import torch  # noqa: F401
+    from wush_int4_kernel_amd import capi as c
+    c.load()
+    return c
+
+
+def test_header_declares_expected_entry_points():
+    syms = declared_symbols()
+    for s in ["wush_quant_int4", "wush_fused_tq", "wush_gemv_int4", "wush_gemm_s4",
+              "wush_gemm_s4_workspace_bytes", "wush_mfma_selftest", "wush_quant_int4_tensor_scale",
+              "wush_gemm_s4_tensor_scale", "wush_abi_version", "wush_error_string"]:
+        assert s in syms, s
+
+
+def test_library_exports_every_declared_symbol(capi):
+    lib = capi.load()
+    for s in declared_symbols():
+        assert hasattr(lib, s), s
+    assert set(declared_symbols()) == set(capi.SIGNATURES)
+    assert lib.wush_abi_version() == 1
+
+
+def test_library_exports_no_undeclared_c_symbols():
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", os.path.join(ROOT, "wush_int4_kernel_amd", "libwush_int4.so")],
+                         capture_output=True, text=True).stdout
+    exported = sorted(set(re.findall(r" T (wush_[a-z0-9_]+)$", out, re.M)))
+    assert exported == declared_symbols()
+
+
+def test_argument_validation_without_device(capi):
+    lib = capi.load()
+    P = ctypes.c_void_p
+    # empty work succeeds without touching the device
+    assert lib.wush_quant_int4(None, 0, None, None, 0, None) == 0
+    assert lib.wush_fused_tq(None, None, None, None, 0, 32, None) == 0
+    assert lib.wush_gemm_s4(None, None, None, None, None, 0, 8, 64, None, 0, None) == 0
+    # bad arguments are rejected before any launch
+    assert lib.wush_quant_int4(None, 0, None, None, 4, None) == INVALID
+    assert lib.wush_quant_int4(P(16), 9, P(16), P(16), 4, None) == INVALID       # dtype
+    assert lib.wush_quant_int4(P(8), 0, P(16), P(16), 4, None) == INVALID        # misaligned x
+    assert lib.wush_fused_tq(P(16), P(16), P(16), P(16), 1, 48, None) == INVALID  # K % 32
+    assert lib.wush_gemv_int4(P(16), P(16), P(16), P(16), P(16), 9, 4, 64, None) == INVALID  # M > 8
+    assert lib.wush_gemv_int4(P(16), P(16), P(16), P(16), P(16), 8, 4, 1 << 20, None) == INVALID  # LDS
+    assert lib.wush_gemm_s4(P(16), P(16), P(16), P(16), P(16), 4, 4, 40, None, 0, None) == INVALID
+    assert lib.wush_gemm_s4_tensor_scale(P(16), P(16), P(16), 4, 4, 1 << 21, 1.0, None, None) == INVALID
+    assert lib.wush_quant_int4_tensor_scale(P(16), P(16), 40, 1.0, None, None) == INVALID
+    assert lib.wush_mfma_selftest(None, None, None, None) == INVALID
+    assert b"invalid argument" in lib.wush_error_string(INVALID)
+
+
+def test_workspace_plan_is_host_only(capi):
+    # split-K only for skinny shapes with few output tiles
+    assert capi.gemm_s4_workspace_bytes(8, 4096, 4096) > 0
+    assert capi.gemm_s4_workspace_bytes(4096, 4096, 4096) == 0
+    assert capi.gemm_s4_workspace_bytes(0, 4096, 4096) == 0
+    assert capi.gemm_s4_workspace_bytes(8, 4096, 40) == 0
+
+
+def test_torch_module_exposes_reference_ops():
+    from my_int4 import _C
+    import my_int4
+    from wush_int4_kernel_amd import _C as C2
+    for op in REFERENCE_OPS:
+        assert callable(getattr(_C, op)), op
+        assert getattr(_C, op) is getattr(C2, op)
+    assert my_int4.quant_int4 is C2.quant_int4
+    assert _C.abi_version() == 1
+
+
+def test_torch_ops_reject_cpu_tensors():
+    import torch
+    from my_int4 import _C
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        _C.quant_int4(x)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        _C.fused_transform_quant_int4(x, torch.zeros(2, 32, 32, dtype=torch.bfloat16))
+    q = torch.zeros(4, 32, dtype=torch.uint8)
+    s = torch.zeros(4, 2, dtype=torch.bfloat16)
+    for op in ["w4a4_gemm_s4", "w4a4_gemv_multi", "w4a4_gemm", "w4a4_gemm_v1", "w4a4_gemm_v2"]:
+        with pytest.raises(RuntimeError, match="CUDA"):
+            getattr(_C, op)(q, s, q, s)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        _C.w4a4_gemm_cutlass(q, q, 1.0)

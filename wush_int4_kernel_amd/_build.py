@@ -1,0 +1,113 @@
+"""Build the two native artefacts of wush_int4_kernel_amd, in place:
+
+* ``libwush_int4.so`` -- every HIP kernel plus the C ABI of
+  ``include/wush_int4.h``, compiled by hipcc for gfx950 only;
+* ``_C<ext-suffix>.so`` -- the torch/pybind11 module that mirrors the
+  reference's ``my_int4._C`` ops and calls the C ABI (g++, no device code).
+
+Numerics flags: no FMA contraction, fp32 denormals kept, correctly rounded
+division and square root (the quantizers are bit-exact with the reference);
+packed-fp32 instructions are disabled.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+import sysconfig
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+BUILD = os.path.join(PKG, "_build")
+LIB = os.path.join(PKG, "libwush_int4.so")
+EXT = os.path.join(PKG, "_C" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+HIP_SOURCES = ["quant.hip", "fused_tq.hip", "gemv.hip", "gemm_s4.hip"]
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-mcode-object-version=5",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    out = subprocess.run(cmd, capture_output=True, text=True)
+    if out.returncode != 0:
+        raise RuntimeError(f"command failed ({out.returncode}): {' '.join(cmd)}\n{out.stdout}\n{out.stderr}")
+    return out
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    return "hipcc"
+
+
+def build_capi(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    cc = hipcc()
+
+    def compile_one(src):
+        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        _run([cc, *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj], verbose)
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=min(4, len(HIP_SOURCES))) as ex:
+        objs = list(ex.map(compile_one, HIP_SOURCES))
+    tmp = LIB + ".tmp"
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_torch_ext(verbose: bool = False) -> str:
+    import torch
+    from torch.utils import cpp_extension
+
+    inc = cpp_extension.include_paths() + [sysconfig.get_paths()["include"], "/opt/rocm/include", INCLUDE]
+    libdirs = cpp_extension.library_paths()
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        "-DTORCH_EXTENSION_NAME=_C", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        *[f"-I{p}" for p in inc],
+        os.path.join(CSRC, "bindings.cpp"),
+        *[f"-L{p}" for p in libdirs],
+        f"-L{PKG}", "-lwush_int4",
+        "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lc10_hip", "-ltorch_hip",
+        "-Wl,-rpath,$ORIGIN",
+        "-o", EXT + ".tmp",
+    ]
+    _run(cmd, verbose)
+    os.replace(EXT + ".tmp", EXT)
+    return EXT
+
+
+def build(verbose: bool = False):
+    """Compile libwush_int4.so, then the torch module that links it."""
+    lib = build_capi(verbose)
+    ext = build_torch_ext(verbose)
+    return lib, ext
+
+
+if __name__ == "__main__":
+    for p in build(verbose="-v" in sys.argv):
+        print("built", p)

@@ -1,0 +1,156 @@
+// fused_tq.hip -- WUSH block-diagonal transform fused with the INT4 group
+// quantization, bit-exact with the reference's sequential form
+// (csrc/fused_tq_int4.cu:27-85; tests/test_sw2.py:12-24):
+//   x'_j = sum_{i=0..31} x_i * T[c][j][i]   (fp32, i ascending, mul then add)
+//   then the quant_int4 chain on the fp32 x' (no bf16 rounding of x').
+// Transformed activations never touch HBM.
+//
+// Two launch shapes, one numerics:
+//  * rows kernel (rows >= 64): lane = row, wavefront = 64 rows of one block c.
+//    T[c] is wave-uniform, so it is read with scalar loads into SGPRs and
+//    every product is v_mul with an SGPR operand: no LDS and no cross-lane
+//    traffic in the 2048-op inner loop.  4 wavefronts of a workgroup take 4
+//    adjacent blocks of the same 64 rows, so each row's 256 B of bf16 input
+//    is consumed by one workgroup.
+//  * small-M kernel (rows < 64, decode): 32 lanes per (row, block), lane j
+//    computes x'_j with T[c][j] read as 64 coalesced bytes and x broadcast
+//    from LDS; the group sums are then re-run in i-order by every lane from
+//    LDS (so they keep the sequential order) and lane pairs pack nibbles.
+#include "wush_device.h"
+#include "../../include/wush_int4.h"
+
+namespace wush {
+
+__device__ __forceinline__ void load_bf16x32(const uint16_t* p, float (&v)[32]) {
+    const uint4* p4 = reinterpret_cast<const uint4*>(p);
+    uint4 r[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = p4[c];
+    const uint32_t* u = reinterpret_cast<const uint32_t*>(r);
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+        v[2 * d] = bf16_to_f32(u[d] & 0xffffu);
+        v[2 * d + 1] = __uint_as_float(u[d] & 0xffff0000u);
+    }
+}
+
+constexpr int kRowsPerWave = 64;
+constexpr int kBlocksPerWg = 4;
+
+__global__ __launch_bounds__(256) void fused_tq_rows_kernel(const uint16_t* __restrict__ x,
+                                                            const uint16_t* __restrict__ t,
+                                                            uint8_t* __restrict__ q,
+                                                            uint16_t* __restrict__ s,
+                                                            int64_t rows, int64_t K) {
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int64_t C = K >> 5;
+    const int64_t c = (int64_t)blockIdx.x * kBlocksPerWg + wave;
+    if (c >= C) return;
+    const int64_t r = (int64_t)blockIdx.y * kRowsPerWave + lane;
+    const bool active = r < rows;
+
+    float xv[32];
+    if (active) {
+        load_bf16x32(x + r * K + c * 32, xv);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) xv[i] = 0.0f;
+    }
+
+    // T[c][j][i] as bf16 pairs (i even in the low half), wave-uniform.
+    const uint32_t* tc = reinterpret_cast<const uint32_t*>(t + c * 1024);
+    float xp[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 16; ++d) {
+            const uint32_t pair = tc[j * 16 + d];
+            acc = acc + xv[2 * d] * bf16_to_f32(pair & 0xffffu);
+            acc = acc + xv[2 * d + 1] * __uint_as_float(pair & 0xffff0000u);
+        }
+        xp[j] = acc;
+    }
+
+    uint32_t w[4];
+    const uint32_t sb = quant_group32(xp, w);
+    if (active) {
+        reinterpret_cast<uint4*>(q + (r * C + c) * 16)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        s[r * C + c] = (uint16_t)sb;
+    }
+}
+
+constexpr int kPairsPerWg = 8;   // (row, block) pairs per 256-thread workgroup
+
+__global__ __launch_bounds__(256) void fused_tq_smallm_kernel(const uint16_t* __restrict__ x,
+                                                              const uint16_t* __restrict__ t,
+                                                              uint8_t* __restrict__ q,
+                                                              uint16_t* __restrict__ s,
+                                                              int64_t rows, int64_t K) {
+    __shared__ float xs[kPairsPerWg][32];
+    __shared__ float xps[kPairsPerWg][32];
+    const int pl = threadIdx.x >> 5;             // pair within the workgroup
+    const int j = threadIdx.x & 31;              // output index within the block
+    const int64_t C = K >> 5;
+    const int64_t p = (int64_t)blockIdx.x * kPairsPerWg + pl;
+    const bool active = p < rows * C;
+    const int64_t r = active ? p / C : 0;
+    const int64_t c = active ? p % C : 0;
+
+    xs[pl][j] = active ? bf16_to_f32(x[r * K + c * 32 + j]) : 0.0f;
+    float tj[32];
+    if (active) {
+        load_bf16x32(t + c * 1024 + j * 32, tj);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) tj[i] = 0.0f;
+    }
+    __syncthreads();
+
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc = acc + xs[pl][i] * tj[i];
+    xps[pl][j] = acc;
+    __syncthreads();
+
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const float v = xps[pl][i];
+        s1 = s1 + v;
+        s2 = s2 + v * v;
+    }
+    float sf;
+    const uint32_t sb = group_scale(s1, s2, &sf);
+    const int code = code_of(acc, sf) & 0xF;
+    const int partner = __shfl_xor(code, 1, 32);
+    if (active) {
+        if ((j & 1) == 0) q[p * 16 + (j >> 1)] = (uint8_t)(code | (partner << 4));
+        if (j == 0) s[p] = (uint16_t)sb;
+    }
+}
+
+}  // namespace wush
+
+extern "C" int wush_fused_tq(const uint16_t* x, const uint16_t* t, uint8_t* q, uint16_t* s,
+                             int64_t rows, int64_t K, hipStream_t stream) {
+    WUSH_REQUIRE(rows >= 0 && K > 0 && K % 32 == 0);
+    if (rows == 0) return (int)hipSuccess;
+    WUSH_REQUIRE(x && t && q && s);
+    WUSH_REQUIRE(((uintptr_t)x & 15u) == 0 && ((uintptr_t)t & 15u) == 0 &&
+                 ((uintptr_t)q & 15u) == 0 && ((uintptr_t)s & 1u) == 0);
+    const int64_t C = K / 32;
+    if (rows < wush::kRowsPerWave) {
+        const int64_t blocks = (rows * C + wush::kPairsPerWg - 1) / wush::kPairsPerWg;
+        WUSH_REQUIRE(blocks <= 0x7fffffffLL);
+        wush::fused_tq_smallm_kernel<<<(unsigned)blocks, 256, 0, stream>>>(x, t, q, s, rows, K);
+    } else {
+        const int64_t gx = (C + wush::kBlocksPerWg - 1) / wush::kBlocksPerWg;
+        const int64_t gy = (rows + wush::kRowsPerWave - 1) / wush::kRowsPerWave;
+        WUSH_REQUIRE(gx <= 0x7fffffffLL && gy <= 65535);
+        wush::fused_tq_rows_kernel<<<dim3((unsigned)gx, (unsigned)gy), 256, 0, stream>>>(x, t, q, s,
+                                                                                         rows, K);
+    }
+    return (int)hipGetLastError();
+}

@@ -1,0 +1,136 @@
+// gemv.hip -- decode W4A4 GEMV for 1 <= M <= 8 (csrc/gemv_int4.cu:23-223).
+//
+//   y[m][n] = sum_g sx[m][g] * sw[n][g] * D[m][n][g],
+//   D[m][n][g] = sum_{k in g} qx[m][k] * qw[n][k]   (exact int32)
+//
+// A pure HBM-streaming kernel: no MFMA.  The packed activations (M*K/2 bytes)
+// and their scales are staged once per workgroup in LDS; every wavefront then
+// streams whole weight rows: lane l takes groups l, l+64, ... so each load
+// instruction of a wavefront reads 1 KiB of contiguous codes (16 B per lane)
+// and 128 B of contiguous scales.  The group dot is 4 v_dot8_i32_i4 on the
+// packed nibbles as stored (element 2k low nibble pairs with element 2k low
+// nibble), the fold is one cvt + one mul + one fma in fp32, and a wavefront
+// reduction finishes each output.  Two weight rows are in flight per
+// wavefront so that each lane keeps 2 x (K/2048) 16-byte loads outstanding.
+#include "wush_device.h"
+#include "../../include/wush_int4.h"
+
+namespace wush {
+
+constexpr int kGemvWaves = 4;
+constexpr int kGemvRowsPerIter = 2;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ int dot32_s4(const uint4& a, const uint4& b) {
+    int d = __builtin_amdgcn_sdot8((int)a.x, (int)b.x, 0, false);
+    d = __builtin_amdgcn_sdot8((int)a.y, (int)b.y, d, false);
+    d = __builtin_amdgcn_sdot8((int)a.z, (int)b.z, d, false);
+    d = __builtin_amdgcn_sdot8((int)a.w, (int)b.w, d, false);
+    return d;
+}
+
+template <int M>
+__global__ __launch_bounds__(256) void gemv_int4_kernel(const uint8_t* __restrict__ xq,
+                                                        const uint16_t* __restrict__ xs,
+                                                        const uint8_t* __restrict__ wq,
+                                                        const uint16_t* __restrict__ ws,
+                                                        uint16_t* __restrict__ y, int N, int K,
+                                                        int rows_per_wave) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int G = K >> 5;
+    const int K2 = K >> 1;
+    uint4* xq_l = reinterpret_cast<uint4*>(smem);                 // [M][G] x 16 B
+    float* xs_l = reinterpret_cast<float*>(smem + (size_t)M * K2); // [M][G]
+
+    const uint4* xq4 = reinterpret_cast<const uint4*>(xq);
+    for (int i = threadIdx.x; i < M * G; i += blockDim.x) xq_l[i] = xq4[i];
+    for (int i = threadIdx.x; i < M * G; i += blockDim.x) xs_l[i] = bf16_to_f32(xs[i]);
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int n_begin = (blockIdx.x * kGemvWaves + wave) * rows_per_wave;
+    const int n_end = min(N, n_begin + rows_per_wave);
+
+    for (int n0 = n_begin; n0 < n_end; n0 += kGemvRowsPerIter) {
+        float acc[kGemvRowsPerIter][M];
+#pragma unroll
+        for (int r = 0; r < kGemvRowsPerIter; ++r)
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+
+        for (int g = lane; g < G; g += 64) {
+            uint4 wv[kGemvRowsPerIter];
+            float swv[kGemvRowsPerIter];
+#pragma unroll
+            for (int r = 0; r < kGemvRowsPerIter; ++r) {
+                const int n = min(n0 + r, n_end - 1);   // duplicate the last row, never store it
+                wv[r] = load_nt16(wq + (size_t)n * K2 + (size_t)g * 16);
+                swv[r] = bf16_to_f32(ws[(size_t)n * G + g]);
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const uint4 xv = xq_l[m * G + g];
+                const float sxv = xs_l[m * G + g];
+#pragma unroll
+                for (int r = 0; r < kGemvRowsPerIter; ++r) {
+                    const int d = dot32_s4(wv[r], xv);
+                    acc[r][m] = __builtin_fmaf((float)d, sxv * swv[r], acc[r][m]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kGemvRowsPerIter; ++r) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float v = wave_sum(acc[r][m]);
+                if (lane == 0 && n0 + r < n_end) y[(size_t)m * N + n0 + r] = f32_to_f16_bits(v);
+            }
+        }
+    }
+}
+
+template <int M>
+static void launch_gemv(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
+                        uint16_t* y, int N, int K, hipStream_t stream) {
+    const int G = K / 32;
+    const size_t smem = (size_t)M * (K / 2) + (size_t)M * G * sizeof(float);
+    // Rows per wavefront: enough workgroups to cover the 256 CUs several times.
+    int rows_per_wave = 8;
+    while (rows_per_wave > 2 && (N + kGemvWaves * rows_per_wave - 1) / (kGemvWaves * rows_per_wave) < 1024)
+        rows_per_wave >>= 1;
+    const int blocks = (N + kGemvWaves * rows_per_wave - 1) / (kGemvWaves * rows_per_wave);
+    gemv_int4_kernel<M><<<blocks, 64 * kGemvWaves, smem, stream>>>(xq, xs, wq, ws, y, N, K, rows_per_wave);
+}
+
+}  // namespace wush
+
+extern "C" int wush_gemv_int4(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq,
+                              const uint16_t* ws, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                              hipStream_t stream) {
+    WUSH_REQUIRE(M >= 1 && M <= 8 && N >= 0 && K > 0 && K % 32 == 0);
+    WUSH_REQUIRE(N <= 0x7fffffffLL && K <= 0x7fffffffLL);
+    if (N == 0) return (int)hipSuccess;
+    WUSH_REQUIRE(xq && xs && wq && ws && y);
+    WUSH_REQUIRE(((uintptr_t)xq & 15u) == 0 && ((uintptr_t)wq & 15u) == 0);
+    WUSH_REQUIRE(((uintptr_t)xs & 1u) == 0 && ((uintptr_t)ws & 1u) == 0 && ((uintptr_t)y & 1u) == 0);
+    // LDS holds M*K/2 code bytes + M*K/32 fp32 scales: 160 KiB per CU bounds K.
+    WUSH_REQUIRE((size_t)M * (K / 2) + (size_t)M * (K / 32) * 4 <= 64 * 1024);
+    const int n = (int)N, k = (int)K;
+    switch (M) {
+        case 1: wush::launch_gemv<1>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 2: wush::launch_gemv<2>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 3: wush::launch_gemv<3>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 4: wush::launch_gemv<4>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 5: wush::launch_gemv<5>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 6: wush::launch_gemv<6>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 7: wush::launch_gemv<7>(xq, xs, wq, ws, y, n, k, stream); break;
+        default: wush::launch_gemv<8>(xq, xs, wq, ws, y, n, k, stream); break;
+    }
+    return (int)hipGetLastError();
+}

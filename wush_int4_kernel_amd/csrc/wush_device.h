@@ -1,0 +1,112 @@
+// wush_device.h -- device helpers shared by the gfx950 kernels.
+//
+// Numerics contract: every source file is compiled with -ffp-contract=off,
+// fp32 denormals kept and correctly rounded '/' and sqrt, so each float
+// expression below is one IEEE operation rounded to nearest even -- the
+// arithmetic of the reference (my_int4/rtn_int4.py:22-55,
+// csrc/quant_int4.cu:59-100).  Explicit __builtin_fmaf is used only where the
+// fused and unfused forms are provably identical.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define WUSH_HOST_DEVICE __host__ __device__ __forceinline__
+
+namespace wush {
+
+constexpr int kGroup = 32;                       // quantization group along K
+// my_int4/rtn_int4.py:19: C_CLIP = 0.35337862372398376 -> fp32 0x3EB4EE0B.
+constexpr float kClip = 0.35337862372398376f;
+// my_int4/rtn_int4.py:44: "+ 1e-8" -> fp32 0x322BCC77.
+constexpr float kEps = 1e-8f;
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+    return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 for non-NaN inputs (the scale is never
+// NaN: a NaN variance selects 1.0).  Same result as torch's .to(bfloat16).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// fp32 -> fp16 bits, round to nearest even (v_cvt_f16_f32).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Group scale from the two sequential sums (rtn_int4.py:39-48):
+// mean = s1/32, var = s2/32 - mean*mean, scale = sqrt(var)*C + 1e-8 if
+// var >= 0 else 1.0; returns the bf16 bits, *sf gets the bf16 value.
+__device__ __forceinline__ uint32_t group_scale(float s1, float s2, float* sf) {
+    float mean = s1 * 0.03125f;                  // exact: power-of-two scaling
+    float var = s2 * 0.03125f - mean * mean;
+    float scale = 1.0f;
+    if (var >= 0.0f) scale = __builtin_sqrtf(var) * kClip + kEps;
+    uint32_t b = f32_to_bf16_rne(scale);
+    *sf = bf16_to_f32(b);
+    return b;
+}
+
+// INT4 code of v under bf16 scale sf: clamp(rint(v / sf), -7, 7), NaN -> 0
+// (rtn_int4.py:50-51; quant_int4.cu:90-93).
+__device__ __forceinline__ int code_of(float v, float sf) {
+    float y = v / sf;
+    float r = __builtin_rintf(y);
+    r = __builtin_fminf(__builtin_fmaxf(r, -7.0f), 7.0f);
+    return (y == y) ? (int)r : 0;
+}
+
+// Quantize 32 fp32 values in registers: sequential sums, scale, 16 packed
+// bytes as 4 dwords (element 2k low nibble of byte k).
+__device__ __forceinline__ uint32_t quant_group32(const float (&v)[32], uint32_t (&w)[4]) {
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        s1 = s1 + v[i];
+        s2 = s2 + v[i] * v[i];
+    }
+    float sf;
+    uint32_t sb = group_scale(s1, s2, &sf);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint32_t acc = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            acc |= (uint32_t)(code_of(v[d * 8 + e], sf) & 0xF) << (4 * e);
+        w[d] = acc;
+    }
+    return sb;
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load with the non-temporal hint (weights are read once).
+__device__ __forceinline__ uint4 load_nt16(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Unpack 8 signed INT4 codes (one dword) into two dwords of int8 that hold
+// 16*code: lo gets the even elements, hi the odd ones.  Exact: 16*[-8,7] fits
+// int8.  Any fixed permutation of k is fine for a dot product as long as both
+// operands use the same one.
+__device__ __forceinline__ void unpack_s4x8_x16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    lo = (w << 4) & 0xF0F0F0F0u;
+    hi = w & 0xF0F0F0F0u;
+}
+
+}  // namespace wush
+
+// Common argument check used by the extern "C" entry points.
+#define WUSH_REQUIRE(cond)                                   \
+    do {                                                     \
+        if (!(cond)) return (int)hipErrorInvalidValue;       \
+    } while (0)
