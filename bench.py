@@ -167,7 +167,15 @@ def main():
             capi.gemv_int4(xq.data_ptr(), xs.data_ptr(), cq.data_ptr(), cs.data_ptr(), y.data_ptr(),
                            M, N, K, stream.cuda_stream)
         torch.cuda.synchronize()
-        print(json.dumps({"kernel_only": "gemv_int4", "launches": args.warmup + args.steps}))
+        # calibration kernel for the HBM counters: a plain 512 MiB device copy
+        src = torch.empty(256 << 20, dtype=torch.int16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": "gemv_int4", "launches": args.warmup + args.steps,
+                          "gemv_algorithmic_bytes": gemv_bytes(M, N, K),
+                          "copy_bytes_each_way": src.numel() * 2}))
         return
 
     # ------------------------------------------------------------- layer sweep
