@@ -10,9 +10,10 @@ synthetic activations, exactly as the reference's official bench chains it
   M <= 8 : fused transform+quant -> w4a4_gemv / w4a4_gemv_multi
   M >  8 : fused transform+quant -> w4a4_gemm_s4
 with the weights pre-quantized (W' = W T^-1, sigma-clip s4 + bf16 scales) and
-resident in HBM.  Each chain is captured in a HIP graph and replayed
-round-robin over several distinct weight copies (> the 256 MB MALL), so every
-step streams the weights from HBM.  `value` is the M=1 layer time (the
+resident in HBM.  One HIP graph holds one chain per distinct weight copy (the copies together
+exceed the 256 MB MALL, so every step streams its weights from HBM), the way a
+model's layer stack is captured; replays are timed and divided by the number of
+steps they hold.  `value` is the M=1 layer time (the
 headline decode point); the other M are reported beside it, each with the
 hipBLASLt bf16 GEMM time at the same shape measured the same way.
 
@@ -137,24 +138,30 @@ def main():
             return lambda: _C.w4a4_gemv_multi(*_C.fused_transform_quant_int4_smallm(X, T), wq_, ws_)
         return lambda: _C.w4a4_gemm_s4(*_C.fused_transform_quant_int4_v3(X, T), wq_, ws_)
 
-    def capture(fn):
-        for _ in range(3):
-            fn()
+    def capture(fns):
+        """One HIP graph holding one layer step per function (one per weight
+        copy), the way a model's decoder stack is captured: the per-replay
+        launch overhead is paid once per len(fns) steps."""
+        for _ in range(2):
+            for fn in fns:
+                fn()
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            fn()
+            for fn in fns:
+                fn()
         return g
 
-    def time_graphs(graphs, steps, warmup):
-        for i in range(warmup):
-            graphs[i % len(graphs)].replay()
+    def time_graph(g, steps_per_replay, steps, warmup):
+        replays = max(1, steps // steps_per_replay)
+        for _ in range(max(1, warmup // steps_per_replay)):
+            g.replay()
         torch.cuda.synchronize()
         t = time.perf_counter()
-        for i in range(steps):
-            graphs[i % len(graphs)].replay()
+        for _ in range(replays):
+            g.replay()
         torch.cuda.synchronize()
-        return (time.perf_counter() - t) / steps
+        return (time.perf_counter() - t) / (replays * steps_per_replay)
 
     # -------------------------------------------------------- kernel-only mode
     if args.kernel_only:
@@ -183,11 +190,11 @@ def main():
     blas_w = None
     for M in Ms:
         X = activations(M, gdev).to(torch.bfloat16).contiguous()
-        graphs = [capture(chain_fn(X, cq, cs, M)) for cq, cs in copies]
+        graph = capture([chain_fn(X, cq, cs, M) for cq, cs in copies])
         steps = args.steps if M <= 64 else max(10, args.steps // 10)
         warm = args.warmup if M <= 64 else max(3, args.warmup // 4)
-        t_int4 = time_graphs(graphs, steps, warm)
-        del graphs
+        t_int4 = time_graph(graph, len(copies), steps, warm)
+        del graph
         entry = {
             "us": round(t_int4 * 1e6, 2),
             "chain": ("fused_tq(smallm)+gemv" if M <= 8 else "fused_tq+gemm_s4"),
@@ -202,11 +209,9 @@ def main():
             if blas_w is None:
                 blas_w = [Wt] + [Wt.clone() for _ in range(1)]
             Xb = X
-            bgraphs = []
-            for Wc in blas_w:
-                bgraphs.append(capture(lambda Wc=Wc: torch.matmul(Xb, Wc.t())))
-            t_blas = time_graphs(bgraphs, steps, warm)
-            del bgraphs
+            bgraph = capture([lambda Wc=Wc: torch.matmul(Xb, Wc.t()) for Wc in blas_w])
+            t_blas = time_graph(bgraph, len(blas_w), steps, warm)
+            del bgraph
             entry["hipblaslt_bf16_us"] = round(t_blas * 1e6, 2)
             entry["speedup_vs_hipblaslt"] = round(t_blas / t_int4, 3)
         layers[f"M={M}"] = entry
@@ -273,7 +278,7 @@ def main():
                 "transformed by this build's WUSH T and sigma-clip quantized",
         "config": {
             "workload": f"Llama-70B FFN layer K={K} N={N}, M=1: fused_tq(smallm) + gemv_int4, "
-                        f"HIP graph, {args.copies} weight copies rotated",
+                        f"one HIP graph of {args.copies} layer steps over distinct weight copies",
             "K": K, "N": N, "M": 1,
         },
         "layers": layers,

@@ -166,16 +166,24 @@ torch::Tensor w4a4_gemm_v2(torch::Tensor xq, torch::Tensor xs, torch::Tensor wq,
     return gemm_2d(xq.reshape({-1, K2}), xs.reshape({-1, G}), wq, ws, K, "w4a4_gemm_v2");
 }
 
-// GEMV for 1 <= M <= 8 on the streaming kernel; shapes the GEMV kernel cannot
-// stage in LDS go to the MFMA GEMM, which computes the same product.
+// Decode product for 1 <= M <= 8.  M <= 5 runs the dot8 streaming GEMV;
+// from M = 6 the int8-MFMA streaming GEMM is faster (its fold work grows with M
+// more slowly than 4 dot8 + 3 fold ops per row and group), and shapes whose
+// activations the GEMV cannot stage in LDS also go to the GEMM.  Both compute
+// the same product: exact int32 group dots folded in fp32.
+constexpr int64_t kGemvMaxM = 5;
+
 torch::Tensor gemv_impl(const torch::Tensor& xq2, const torch::Tensor& xs2, const torch::Tensor& wq,
                         const torch::Tensor& ws, int64_t M, int64_t K, const char* op) {
     const int64_t N = wq.size(0);
     const at::hip::OptionalHIPGuardMasqueradingAsCUDA guard(xq2.device());
     auto y = torch::empty({M, N}, torch::dtype(torch::kHalf).device(xq2.device()));
-    int st = wush_gemv_int4(ptr<uint8_t>(xq2), ptr<uint16_t>(xs2), ptr<uint8_t>(wq), ptr<uint16_t>(ws),
+    const bool lds_fits = M * (K / 2) + M * (K / 32) * 4 <= 64 * 1024;
+    int st = (int)hipErrorInvalidValue;
+    if (M <= kGemvMaxM && lds_fits)
+        st = wush_gemv_int4(ptr<uint8_t>(xq2), ptr<uint16_t>(xs2), ptr<uint8_t>(wq), ptr<uint16_t>(ws),
                             ptr<uint16_t>(y), M, N, K, current_stream(xq2));
-    if (st == (int)hipErrorInvalidValue && M * (K / 2) + M * (K / 32) * 4 > 64 * 1024) {
+    if (st == (int)hipErrorInvalidValue && (M > kGemvMaxM || !lds_fits)) {
         const size_t wsb = wush_gemm_s4_workspace_bytes(M, N, K);
         torch::Tensor work;
         if (wsb) work = torch::empty({(int64_t)wsb}, torch::dtype(torch::kUInt8).device(xq2.device()));

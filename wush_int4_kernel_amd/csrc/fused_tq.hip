@@ -12,7 +12,9 @@
 //    traffic in the 2048-op inner loop.  4 wavefronts of a workgroup take 4
 //    adjacent blocks of the same 64 rows, so each row's 256 B of bf16 input
 //    is consumed by one workgroup.
-//  * small-M kernel (rows < 64, decode): 32 lanes per (row, block), lane j
+//  * small-M kernel (rows < 64, decode): 32 lanes per (row, block), two
+//    pairs per one-wavefront workgroup so a decode row spreads over K/64 CUs;
+//    lane j
 //    computes x'_j with T[c][j] read as 64 coalesced bytes and x broadcast
 //    from LDS; the group sums are then re-run in i-order by every lane from
 //    LDS (so they keep the sequential order) and lane pairs pack nibbles.
@@ -81,9 +83,9 @@ __global__ __launch_bounds__(256) void fused_tq_rows_kernel(const uint16_t* __re
     }
 }
 
-constexpr int kPairsPerWg = 8;   // (row, block) pairs per 256-thread workgroup
+constexpr int kPairsPerWg = 2;   // (row, block) pairs per one-wavefront workgroup
 
-__global__ __launch_bounds__(256) void fused_tq_smallm_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(64) void fused_tq_smallm_kernel(const uint16_t* __restrict__ x,
                                                               const uint16_t* __restrict__ t,
                                                               uint8_t* __restrict__ q,
                                                               uint16_t* __restrict__ s,
@@ -144,7 +146,7 @@ extern "C" int wush_fused_tq(const uint16_t* x, const uint16_t* t, uint8_t* q, u
     if (rows < wush::kRowsPerWave) {
         const int64_t blocks = (rows * C + wush::kPairsPerWg - 1) / wush::kPairsPerWg;
         WUSH_REQUIRE(blocks <= 0x7fffffffLL);
-        wush::fused_tq_smallm_kernel<<<(unsigned)blocks, 256, 0, stream>>>(x, t, q, s, rows, K);
+        wush::fused_tq_smallm_kernel<<<(unsigned)blocks, 64, 0, stream>>>(x, t, q, s, rows, K);
     } else {
         const int64_t gx = (C + wush::kBlocksPerWg - 1) / wush::kBlocksPerWg;
         const int64_t gy = (rows + wush::kRowsPerWave - 1) / wush::kRowsPerWave;

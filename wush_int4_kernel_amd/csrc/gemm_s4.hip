@@ -27,35 +27,42 @@ namespace wush {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int kStageGroups = 4;                  // groups per LDS stage
 constexpr int kPlanePad = 32;                    // bytes of padding per (group, half) plane
 
-template <int TM, int TN>
+// LDS layout of one pipeline buffer: codes fragment-major
+// [group][k-half][row][8 B] (+ padding per plane) so the MFMA operand reads
+// (lane = row, 8 B) are conflict-free, then fp32 scales [group][row].
+template <int TM, int TN, int SG>
 struct GemmSmem {
     static constexpr int kAPlane = TM * 8 + kPlanePad;
     static constexpr int kBPlane = TN * 8 + kPlanePad;
-    static constexpr int kACodes = kStageGroups * 2 * kAPlane;
-    static constexpr int kBCodes = kStageGroups * 2 * kBPlane;
-    static constexpr int kAScale = kStageGroups * TM * 4;
-    static constexpr int kBScale = kStageGroups * TN * 4;
+    static constexpr int kACodes = SG * 2 * kAPlane;
+    static constexpr int kBCodes = SG * 2 * kBPlane;
+    static constexpr int kAScale = SG * TM * 4;
+    static constexpr int kBScale = SG * TN * 4;
     static constexpr int kBuf = kACodes + kBCodes + kAScale + kBScale;
     static constexpr int kBytes = 2 * kBuf;
 };
 
 // Global -> register prefetch of one stage, spread over the 256 threads.
-template <int TM, int TN>
+// Chunk id -> (row = id / SG, group = id % SG): SG consecutive threads read
+// one row's SG*16 contiguous code bytes, so with SG = 8 every wavefront load
+// instruction reads eight whole 128-byte lines.
+template <int TM, int TN, int SG>
 struct StageRegs {
-    static constexpr int kAChunks = (TM * kStageGroups + 255) / 256;
-    static constexpr int kBChunks = (TN * kStageGroups + 255) / 256;
-    static constexpr int kAScal = (TM * kStageGroups + 255) / 256;
-    static constexpr int kBScal = (TN * kStageGroups + 255) / 256;
+    static constexpr int kAChunks = (TM * SG + 255) / 256;
+    static constexpr int kBChunks = (TN * SG + 255) / 256;
     uint4 a[kAChunks];
     uint4 b[kBChunks];
-    float sa[kAScal];
-    float sb[kBScal];
+    float sa[kAChunks];
+    float sb[kBChunks];
 };
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool PER_TENSOR>
+// BM x BN 32x32 blocks per wavefront, WAVES_M x WAVES_N wavefronts, SG groups
+// per stage, MR = rows of each 32-row block that can hold output (the fold is
+// skipped for accumulator registers of rows >= MR: at decode M <= 8 only a
+// quarter of the MFMA rows are real).
+template <int BM, int BN, int WAVES_M, int WAVES_N, int SG, int MR, bool PER_TENSOR>
 __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict__ xq,
                                                       const uint16_t* __restrict__ xs,
                                                       const uint8_t* __restrict__ wq,
@@ -65,10 +72,12 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
                                                       int M, int N, int K, int groups_per_split,
                                                       float alpha, const float* __restrict__ alpha_dev) {
     static_assert(WAVES_M * WAVES_N == 4, "4 wavefronts per workgroup");
+    static_assert(MR % 8 == 0 && MR <= 32, "fold rows");
     constexpr int TM = 32 * BM * WAVES_M;
     constexpr int TN = 32 * BN * WAVES_N;
-    using S = GemmSmem<TM, TN>;
-    using R = StageRegs<TM, TN>;
+    constexpr int NR = MR / 2;
+    using S = GemmSmem<TM, TN, SG>;
+    using R = StageRegs<TM, TN, SG>;
     extern __shared__ __align__(16) uint8_t smem[];
 
     const int tid = threadIdx.x;
@@ -85,98 +94,68 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
     const int K2 = K >> 1;
     const int g_begin = blockIdx.z * groups_per_split;
     const int g_end = min(G, g_begin + groups_per_split);
-    const int n_stages = (g_end - g_begin + kStageGroups - 1) / kStageGroups;
+    const int n_stages = (g_end - g_begin + SG - 1) / SG;
 
     auto load_stage = [&](int st, R& r) {
-        const int gs = g_begin + st * kStageGroups;
+        const int gs = g_begin + st * SG;
 #pragma unroll
         for (int c = 0; c < R::kAChunks; ++c) {
             const int id = tid + c * 256;
-            const int row = id >> 2, g = id & 3;
+            const int row = id / SG, g = id % SG;
             const int gm = m0 + row, gg = gs + g;
-            r.a[c] = (row < TM && gm < M && gg < g_end)
-                         ? *reinterpret_cast<const uint4*>(xq + (size_t)gm * K2 + (size_t)gg * 16)
-                         : make_uint4(0, 0, 0, 0);
+            const bool ok = row < TM && gm < M && gg < g_end;
+            r.a[c] = ok ? *reinterpret_cast<const uint4*>(xq + (size_t)gm * K2 + (size_t)gg * 16)
+                        : make_uint4(0, 0, 0, 0);
+            if constexpr (!PER_TENSOR) r.sa[c] = ok ? bf16_to_f32(xs[(size_t)gm * G + gg]) : 0.0f;
         }
 #pragma unroll
         for (int c = 0; c < R::kBChunks; ++c) {
             const int id = tid + c * 256;
-            const int row = id >> 2, g = id & 3;
+            const int row = id / SG, g = id % SG;
             const int gn = n0 + row, gg = gs + g;
-            r.b[c] = (row < TN && gn < N && gg < g_end)
-                         ? load_nt16(wq + (size_t)gn * K2 + (size_t)gg * 16)
-                         : make_uint4(0, 0, 0, 0);
-        }
-        if constexpr (!PER_TENSOR) {
-#pragma unroll
-            for (int c = 0; c < R::kAScal; ++c) {
-                const int id = tid + c * 256;
-                const int row = id >> 2, g = id & 3;
-                const int gm = m0 + row, gg = gs + g;
-                r.sa[c] = (row < TM && gm < M && gg < g_end) ? bf16_to_f32(xs[(size_t)gm * G + gg]) : 0.0f;
-            }
-#pragma unroll
-            for (int c = 0; c < R::kBScal; ++c) {
-                const int id = tid + c * 256;
-                const int row = id >> 2, g = id & 3;
-                const int gn = n0 + row, gg = gs + g;
-                r.sb[c] = (row < TN && gn < N && gg < g_end) ? bf16_to_f32(ws[(size_t)gn * G + gg]) : 0.0f;
-            }
+            const bool ok = row < TN && gn < N && gg < g_end;
+            r.b[c] = ok ? *reinterpret_cast<const uint4*>(wq + (size_t)gn * K2 + (size_t)gg * 16)
+                        : make_uint4(0, 0, 0, 0);
+            if constexpr (!PER_TENSOR) r.sb[c] = ok ? bf16_to_f32(ws[(size_t)gn * G + gg]) : 0.0f;
         }
     };
 
     auto store_stage = [&](int buf, const R& r) {
         uint8_t* base = smem + buf * S::kBuf;
+        uint8_t* bbase = base + S::kACodes;
+        float* sa = reinterpret_cast<float*>(base + S::kACodes + S::kBCodes);
+        float* sbp = sa + SG * TM;
 #pragma unroll
         for (int c = 0; c < R::kAChunks; ++c) {
             const int id = tid + c * 256;
-            const int row = id >> 2, g = id & 3;
+            const int row = id / SG, g = id % SG;
             if (row < TM) {
-                uint2* p0 = reinterpret_cast<uint2*>(base + (g * 2 + 0) * S::kAPlane + row * 8);
-                uint2* p1 = reinterpret_cast<uint2*>(base + (g * 2 + 1) * S::kAPlane + row * 8);
-                *p0 = make_uint2(r.a[c].x, r.a[c].y);
-                *p1 = make_uint2(r.a[c].z, r.a[c].w);
+                *reinterpret_cast<uint2*>(base + (g * 2 + 0) * S::kAPlane + row * 8) = make_uint2(r.a[c].x, r.a[c].y);
+                *reinterpret_cast<uint2*>(base + (g * 2 + 1) * S::kAPlane + row * 8) = make_uint2(r.a[c].z, r.a[c].w);
+                if constexpr (!PER_TENSOR) sa[g * TM + row] = r.sa[c];
             }
         }
-        uint8_t* bbase = base + S::kACodes;
 #pragma unroll
         for (int c = 0; c < R::kBChunks; ++c) {
             const int id = tid + c * 256;
-            const int row = id >> 2, g = id & 3;
+            const int row = id / SG, g = id % SG;
             if (row < TN) {
-                uint2* p0 = reinterpret_cast<uint2*>(bbase + (g * 2 + 0) * S::kBPlane + row * 8);
-                uint2* p1 = reinterpret_cast<uint2*>(bbase + (g * 2 + 1) * S::kBPlane + row * 8);
-                *p0 = make_uint2(r.b[c].x, r.b[c].y);
-                *p1 = make_uint2(r.b[c].z, r.b[c].w);
-            }
-        }
-        if constexpr (!PER_TENSOR) {
-            float* sa = reinterpret_cast<float*>(base + S::kACodes + S::kBCodes);
-            float* sbp = sa + kStageGroups * TM;
-#pragma unroll
-            for (int c = 0; c < R::kAScal; ++c) {
-                const int id = tid + c * 256;
-                const int row = id >> 2, g = id & 3;
-                if (row < TM) sa[g * TM + row] = r.sa[c];
-            }
-#pragma unroll
-            for (int c = 0; c < R::kBScal; ++c) {
-                const int id = tid + c * 256;
-                const int row = id >> 2, g = id & 3;
-                if (row < TN) sbp[g * TN + row] = r.sb[c];
+                *reinterpret_cast<uint2*>(bbase + (g * 2 + 0) * S::kBPlane + row * 8) = make_uint2(r.b[c].x, r.b[c].y);
+                *reinterpret_cast<uint2*>(bbase + (g * 2 + 1) * S::kBPlane + row * 8) = make_uint2(r.b[c].z, r.b[c].w);
+                if constexpr (!PER_TENSOR) sbp[g * TN + row] = r.sb[c];
             }
         }
     };
 
     // Accumulators: fp32 (group-scaled) or int32 (per-tensor, whole K).
-    float acc[BM][BN][16];
+    float acc[BM][BN][NR];
     v16i iacc[BM][BN];
 #pragma unroll
     for (int bm = 0; bm < BM; ++bm)
 #pragma unroll
         for (int bn = 0; bn < BN; ++bn) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) acc[bm][bn][j] = 0.0f;
+            for (int j = 0; j < NR; ++j) acc[bm][bn][j] = 0.0f;
             iacc[bm][bn] = (v16i){0};
         }
 
@@ -184,10 +163,10 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
         const uint8_t* base = smem + buf * S::kBuf;
         const uint8_t* bbase = base + S::kACodes;
         const float* sa = reinterpret_cast<const float*>(base + S::kACodes + S::kBCodes);
-        const float* sbp = sa + kStageGroups * TM;
-        const int groups_here = min(kStageGroups, g_end - (g_begin + st * kStageGroups));
+        const float* sbp = sa + SG * TM;
+        const int groups_here = min(SG, g_end - (g_begin + st * SG));
 #pragma unroll
-        for (int g = 0; g < kStageGroups; ++g) {
+        for (int g = 0; g < SG; ++g) {
             if (g >= groups_here) break;
             v4i afr[BM], bfr[BN];
 #pragma unroll
@@ -221,10 +200,10 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
                 for (int bn = 0; bn < BN; ++bn) swv[bn] = sbp[g * TN + wn + bn * 32 + l32];
 #pragma unroll
                 for (int bm = 0; bm < BM; ++bm) {
-                    // rows of this lane: 8*(j/4) + 4*half + (j%4), j = 0..15
-                    float sxv[16];
+                    // rows of this lane: 8*(j/4) + 4*half + (j%4), j = 0..NR-1
+                    float sxv[NR];
 #pragma unroll
-                    for (int jb = 0; jb < 4; ++jb) {
+                    for (int jb = 0; jb < NR / 4; ++jb) {
                         const float4 v = *reinterpret_cast<const float4*>(
                             sa + g * TM + wm + bm * 32 + jb * 8 + half * 4);
                         sxv[jb * 4 + 0] = v.x;
@@ -237,7 +216,7 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
                         const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[bm], bfr[bn],
                                                                              (v16i){0}, 0, 0, 0);
 #pragma unroll
-                        for (int j = 0; j < 16; ++j)
+                        for (int j = 0; j < NR; ++j)
                             acc[bm][bn][j] = __builtin_fmaf((float)d[j], sxv[j] * swv[bn], acc[bm][bn][j]);
                     }
                 }
@@ -268,7 +247,7 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
         for (int bn = 0; bn < BN; ++bn) {
             const int col = n0 + wn + bn * 32 + l32;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
+            for (int j = 0; j < (PER_TENSOR ? 16 : NR); ++j) {
                 const int row = m0 + wm + bm * 32 + 8 * (j >> 2) + 4 * half + (j & 3);
                 if (row < M && col < N) {
                     float v;
@@ -283,6 +262,206 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
                 }
             }
         }
+}
+
+// ------------------------------------------------ streaming kernel (M <= 32)
+// Decode-sized M: the run time is the weight stream, so each wavefront owns
+// 32*NB weight rows and streams its K slice with PF stages (8 groups = one
+// 128-byte line per row) of loads in flight in registers -- under full load
+// HBM needs ~150-200 KB outstanding per CU.  A stage of weights is read with
+// fully coalesced loads (lane i: row 8j + i/8, line chunk i%8) and transposed
+// through a wavefront-private LDS slab into the MFMA operand layout
+// [group][k-half][row][8 B]; the slab's plane stride (272 B) makes both the
+// transposing writes and the fragment reads bank-conflict-free, and no
+// workgroup barrier is needed.  Activations (<= 32 rows, L2-resident) are
+// loaded as whole 16-byte groups and re-paired across lane halves with
+// v_permlane32_swap.  Weight scales arrive as one 16-byte load per row and
+// stage; x scales for the slice sit in LDS.  Requires K % 256 == 0 and slices
+// of whole stages.
+constexpr int kStreamSG = 8;                     // groups per stage
+constexpr int kStreamPlane = 32 * 8 + 16;        // bytes per (group, half) plane of a 32-row block
+
+__device__ __forceinline__ void swap_halves(uint4& v) {
+    // v_permlane32_swap(vdst, vsrc) exchanges vdst of lanes 32-63 with vsrc of
+    // lanes 0-31.  With lane l holding group g and lane l+32 group g+1 of the
+    // same row, afterwards (x,y) hold k-half (l/32) of group g and (z,w) the
+    // same k-half of group g+1.
+    auto a = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+    auto b = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+    v.x = a[0]; v.z = a[1];
+    v.y = b[0]; v.w = b[1];
+}
+
+template <int NB>
+struct StreamStage {
+    uint4 w[NB][4];     // weight line chunks: row 8j + lane/8, group lane%8
+    uint4 x[4];         // activation groups 2t + half of row lane%32
+    uint4 sw[NB];       // 8 bf16 weight scales of this lane's column
+};
+
+template <int MR, int NB, int PF>
+__global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __restrict__ xq,
+                                                             const uint16_t* __restrict__ xs,
+                                                             const uint8_t* __restrict__ wq,
+                                                             const uint16_t* __restrict__ ws,
+                                                             uint16_t* __restrict__ y,
+                                                             float* __restrict__ partial,
+                                                             int M, int N, int K, int groups_per_split) {
+    constexpr int NR = MR / 2;
+    constexpr int kSlab = NB * kStreamSG * 2 * kStreamPlane;    // bytes of one wavefront's slab
+    static_assert(MR % 8 == 0 && MR <= 32, "fold rows");
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int half = lane >> 5;
+    const int l32 = lane & 31;
+    const int G = K >> 5;
+    const int K2 = K >> 1;
+    const int g_begin = blockIdx.y * groups_per_split;
+    const int g_end = min(G, g_begin + groups_per_split);
+    const int gcount = g_end - g_begin;          // multiple of kStreamSG
+    float* sx_l = reinterpret_cast<float*>(smem);                       // [gcount][32]
+    uint8_t* slab = smem + (size_t)groups_per_split * 32 * sizeof(float) + (size_t)wave * kSlab;
+
+    for (int i = threadIdx.x; i < gcount * 32; i += 256) {
+        const int g = i >> 5, m = i & 31;
+        sx_l[i] = (m < M) ? bf16_to_f32(xs[(size_t)m * G + g_begin + g]) : 0.0f;
+    }
+    __syncthreads();
+
+    const int nb0 = (blockIdx.x * 4 + wave) * NB;
+    if (nb0 * 32 >= N) return;
+
+    // Per-lane base pointers; out-of-range rows are clamped to valid rows and
+    // their data masked, so the streaming loop has no branches.
+    const uint8_t* wp[NB][4];
+    uint32_t wmask[NB][4];
+    const uint16_t* sp[NB];
+    uint32_t smask[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = (nb0 + b) * 32 + 8 * j + (lane >> 3);
+            wmask[b][j] = n < N ? 0xffffffffu : 0u;
+            wp[b][j] = wq + (size_t)(n < N ? n : N - 1) * K2 + (size_t)(g_begin + (lane & 7)) * 16;
+        }
+        const int n = (nb0 + b) * 32 + l32;
+        smask[b] = n < N ? 0xffffffffu : 0u;
+        sp[b] = ws + (size_t)(n < N ? n : N - 1) * G + g_begin;
+    }
+    const uint32_t xmask = l32 < M ? 0xffffffffu : 0u;
+    const uint8_t* xp = xq + (size_t)(l32 < M ? l32 : 0) * K2 + (size_t)(g_begin + half) * 16;
+
+    float acc[NB][NR];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < NR; ++j) acc[b][j] = 0.0f;
+
+    const int nst = gcount / kStreamSG;
+    auto load = [&](int st, StreamStage<NB>& S) {
+        const size_t off = (size_t)st * (kStreamSG * 16);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) S.w[b][j] = load_nt16(wp[b][j] + off);
+            S.sw[b] = *reinterpret_cast<const uint4*>(sp[b] + st * kStreamSG);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) S.x[t] = *reinterpret_cast<const uint4*>(xp + off + (size_t)t * 32);
+    };
+
+    auto process = [&](int st, StreamStage<NB>& S) {
+        // 1. transpose this stage's weights into the slab
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint4 v = S.w[b][j];
+                const int row = 8 * j + (lane >> 3), g = lane & 7;
+                uint8_t* base = slab + b * (kStreamSG * 2 * kStreamPlane) + row * 8;
+                *reinterpret_cast<uint2*>(base + (g * 2 + 0) * kStreamPlane) =
+                    make_uint2(v.x & wmask[b][j], v.y & wmask[b][j]);
+                *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) =
+                    make_uint2(v.z & wmask[b][j], v.w & wmask[b][j]);
+            }
+        }
+        // 2. activation operands of the 8 groups
+        v4i A[kStreamSG];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint4 v = S.x[t];
+            v.x &= xmask; v.y &= xmask; v.z &= xmask; v.w &= xmask;
+            swap_halves(v);
+            uint32_t a0, a1, a2, a3, a4, a5, a6, a7;
+            unpack_s4x8_x16(v.x, a0, a1);
+            unpack_s4x8_x16(v.y, a2, a3);
+            unpack_s4x8_x16(v.z, a4, a5);
+            unpack_s4x8_x16(v.w, a6, a7);
+            A[2 * t] = (v4i){(int)a0, (int)a1, (int)a2, (int)a3};
+            A[2 * t + 1] = (v4i){(int)a4, (int)a5, (int)a6, (int)a7};
+        }
+        // 3. per group: weight fragment from the slab, MFMA, fold
+        const int gi0 = st * kStreamSG;
+#pragma unroll
+        for (int g = 0; g < kStreamSG; ++g) {
+            float sxv[NR];
+#pragma unroll
+            for (int jb = 0; jb < NR / 4; ++jb) {
+                const float4 u = *reinterpret_cast<const float4*>(sx_l + (gi0 + g) * 32 + 8 * jb + 4 * half);
+                sxv[jb * 4 + 0] = u.x; sxv[jb * 4 + 1] = u.y; sxv[jb * 4 + 2] = u.z; sxv[jb * 4 + 3] = u.w;
+            }
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const uint2 w = *reinterpret_cast<const uint2*>(
+                    slab + b * (kStreamSG * 2 * kStreamPlane) + (g * 2 + half) * kStreamPlane + l32 * 8);
+                uint32_t b0, b1, b2, b3;
+                unpack_s4x8_x16(w.x, b0, b1);
+                unpack_s4x8_x16(w.y, b2, b3);
+                const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
+                const uint32_t sw2 = (&S.sw[b].x)[g >> 1] & smask[b];
+                const float swv = (g & 1) ? __uint_as_float(sw2 & 0xffff0000u) : bf16_to_f32(sw2 & 0xffffu);
+                const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[g], B, (v16i){0}, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < NR; ++j)
+                    acc[b][j] = __builtin_fmaf((float)d[j], sxv[j] * swv, acc[b][j]);
+            }
+        }
+    };
+
+    StreamStage<NB> buf[PF];
+#pragma unroll
+    for (int d = 0; d < PF; ++d) load(min(d, nst - 1), buf[d]);
+    int st = 0;
+    for (; st + PF <= nst; st += PF) {
+#pragma unroll
+        for (int d = 0; d < PF; ++d) {
+            process(st + d, buf[d]);
+            load(min(st + d + PF, nst - 1), buf[d]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < PF - 1; ++d)
+        if (st + d < nst) process(st + d, buf[d]);
+
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int col = (nb0 + b) * 32 + l32;
+        if (col >= N) continue;
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+            const int row = 8 * (j >> 2) + 4 * half + (j & 3);
+            if (row < M) {
+                const float v = acc[b][j] * (1.0f / 256.0f);
+                if (partial != nullptr)
+                    partial[((size_t)blockIdx.y * M + row) * N + col] = v;
+                else
+                    y[(size_t)row * N + col] = f32_to_f16_bits(v);
+            }
+        }
+    }
 }
 
 // Sum the split-K partials in slice order and convert to fp16.
@@ -325,31 +504,69 @@ __global__ void mfma_selftest_kernel(const int8_t* __restrict__ a, const int8_t*
 
 // ---------------------------------------------------------------- planning
 struct Plan {
-    int cfg;        // 0: 32x128 (skinny), 1: 64x128, 2: 128x128
+    int cfg;        // 0: 32x128 (M <= 32), 1: 64x128, 2: 128x128, 3: streaming (M <= 32)
+    int mr;         // fold rows per 32-row block (cfg 0)
     int splits;
     int groups_per_split;
-    int tm, tn;
+    int tm, tn, sg;
 };
+
+#ifndef WUSH_STREAM_PF
+#define WUSH_STREAM_PF 2
+#endif
+constexpr int kStreamNB = 1;
+constexpr int kStreamPF = WUSH_STREAM_PF;        // stages of loads in flight per wavefront
+constexpr size_t kStreamLdsMax = 64 * 1024;
+
+static size_t stream_smem(int64_t gps) {
+    return (size_t)gps * 32 * sizeof(float) + 4 * (size_t)kStreamNB * kStreamSG * 2 * kStreamPlane;
+}
 
 static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available, bool allow_split) {
     Plan p;
+    p.mr = 32;
+    const int64_t G0 = K / 32;
+    if (allow_split && M <= 32 && K % 256 == 0) {
+        // streaming kernel: one wavefront per 32*kStreamNB weight rows
+        p.cfg = 3; p.tm = 32; p.tn = 4 * kStreamNB * 32; p.sg = kStreamSG;
+        p.mr = (int)((M + 7) / 8 * 8);
+        const int64_t waves = (N + 32 * kStreamNB - 1) / (32 * kStreamNB);
+        int s = 1;
+        while (s < 16 && waves * s < 2048 && G0 / (2 * s) >= 4 * kStreamSG) s *= 2;
+        int64_t gps = (G0 + s - 1) / s;
+        gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
+        while (stream_smem(gps) > kStreamLdsMax && gps > kStreamSG) {
+            s *= 2;
+            gps = (G0 + s - 1) / s;
+            gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
+        }
+        s = (int)((G0 + gps - 1) / gps);
+        const bool ws_ok = s == 1 || (size_t)s * (size_t)M * (size_t)N * sizeof(float) <= ws_bytes_available;
+        if (ws_ok && stream_smem(gps) <= kStreamLdsMax) {
+            p.splits = s;
+            p.groups_per_split = (int)gps;
+            return p;
+        }
+        p.mr = 32;
+    }
     if (M <= 32) {
-        p.cfg = 0; p.tm = 32; p.tn = 128;
+        p.cfg = 0; p.tm = 32; p.tn = 128; p.sg = 8;
+        p.mr = (int)((M + 7) / 8 * 8);
     } else if (M <= 64) {
-        p.cfg = 1; p.tm = 64; p.tn = 128;
+        p.cfg = 1; p.tm = 64; p.tn = 128; p.sg = 8;
     } else {
-        p.cfg = 2; p.tm = 128; p.tn = 128;
+        p.cfg = 2; p.tm = 128; p.tn = 128; p.sg = 4;
     }
     const int64_t G = K / 32;
     const int64_t tiles = ((M + p.tm - 1) / p.tm) * ((N + p.tn - 1) / p.tn);
     int s = 1;
     if (allow_split) {
-        // Aim for >= 2 workgroups per CU (256 CUs) while each slice keeps
-        // at least 8 stages of K.
-        while (s < 16 && tiles * s < 512 && G / (2 * s) >= 8 * kStageGroups) s *= 2;
+        // Aim for >= 3 workgroups per CU (256 CUs) while each slice keeps
+        // at least 4 stages of K.
+        while (s < 16 && tiles * s < 768 && G / (2 * s) >= 4 * p.sg) s *= 2;
     }
     int64_t gps = (G + s - 1) / s;
-    gps = (gps + kStageGroups - 1) / kStageGroups * kStageGroups;
+    gps = (gps + p.sg - 1) / p.sg * p.sg;
     s = (int)((G + gps - 1) / gps);
     if (s > 1 && (size_t)s * (size_t)M * (size_t)N * sizeof(float) > ws_bytes_available) {
         s = 1;
@@ -360,14 +577,15 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
     return p;
 }
 
-template <int BM, int BN, int WM, int WN, bool PT>
+template <int BM, int BN, int WM, int WN, int SG, int MR, bool PT>
 static void launch_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                         uint16_t* y, float* partial, int M, int N, int K, const Plan& p, float alpha,
                         const float* alpha_dev, hipStream_t stream) {
     constexpr int TM = 32 * BM * WM, TN = 32 * BN * WN;
-    const size_t smem = GemmSmem<TM, TN>::kBytes;
+    const size_t smem = GemmSmem<TM, TN, SG>::kBytes;
+    static_assert(GemmSmem<TM, TN, SG>::kBytes <= 64 * 1024, "LDS budget");
     dim3 grid((unsigned)((N + TN - 1) / TN), (unsigned)((M + TM - 1) / TM), (unsigned)p.splits);
-    gemm_s4_kernel<BM, BN, WM, WN, PT><<<grid, 256, smem, stream>>>(
+    gemm_s4_kernel<BM, BN, WM, WN, SG, MR, PT><<<grid, 256, smem, stream>>>(
         xq, xs, wq, ws, y, partial, M, N, K, p.groups_per_split, alpha, alpha_dev);
 }
 
@@ -379,10 +597,30 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     WUSH_REQUIRE((N + p.tn - 1) / p.tn <= 0x7fffffffLL && (M + p.tm - 1) / p.tm <= 65535);
     float* partial = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int m = (int)M, n = (int)N, k = (int)K;
-    switch (p.cfg) {
-        case 0: launch_gemm<1, 1, 1, 4, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream); break;
-        case 1: launch_gemm<1, 2, 2, 2, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream); break;
-        default: launch_gemm<2, 2, 2, 2, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream); break;
+    if (p.cfg == 3) {
+        if constexpr (!PT) {
+            const size_t smem = stream_smem(p.groups_per_split);
+            dim3 grid((unsigned)((N + p.tn - 1) / p.tn), (unsigned)p.splits);
+            switch (p.mr) {
+                case 8: gemm_s4_stream_kernel<8, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                case 16: gemm_s4_stream_kernel<16, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                case 24: gemm_s4_stream_kernel<24, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                default: gemm_s4_stream_kernel<32, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+            }
+        }
+    } else if (p.cfg == 0) {
+        if (PT || p.mr == 32)
+            launch_gemm<1, 1, 1, 4, 8, 32, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
+        else if (p.mr == 8)
+            launch_gemm<1, 1, 1, 4, 8, 8, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
+        else if (p.mr == 16)
+            launch_gemm<1, 1, 1, 4, 8, 16, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
+        else
+            launch_gemm<1, 1, 1, 4, 8, 24, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
+    } else if (p.cfg == 1) {
+        launch_gemm<1, 2, 2, 2, 8, 32, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
+    } else {
+        launch_gemm<2, 2, 2, 2, 4, 32, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
     }
     if (p.splits > 1) {
         const int64_t MN = M * N;

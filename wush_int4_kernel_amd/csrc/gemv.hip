@@ -18,7 +18,6 @@
 namespace wush {
 
 constexpr int kGemvWaves = 4;
-constexpr int kGemvRowsPerIter = 2;
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -34,7 +33,20 @@ __device__ __forceinline__ int dot32_s4(const uint4& a, const uint4& b) {
     return d;
 }
 
-template <int M>
+// One wavefront streams the weight rows [n_begin, n_end), R rows at a time.
+// GPL = groups per lane (K/2048): when it is known at compile time all R*GPL
+// 16-byte weight loads of a chunk are issued together and the next chunk is
+// prefetched while the current one is reduced, so ~2*R*GPL KiB stay in flight
+// per wavefront.  The first chunk is requested before the activations are
+// staged in LDS (weights do not depend on them).  GPL == 0 is the generic
+// any-K loop.
+template <int R, int GPL>
+struct GemvChunk {
+    uint4 w[R][GPL];
+    uint32_t s[R][GPL];
+};
+
+template <int M, int R, int GPL>
 __global__ __launch_bounds__(256) void gemv_int4_kernel(const uint8_t* __restrict__ xq,
                                                         const uint16_t* __restrict__ xs,
                                                         const uint8_t* __restrict__ wq,
@@ -47,65 +59,146 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const uint8_t* __restric
     uint4* xq_l = reinterpret_cast<uint4*>(smem);                 // [M][G] x 16 B
     float* xs_l = reinterpret_cast<float*>(smem + (size_t)M * K2); // [M][G]
 
-    const uint4* xq4 = reinterpret_cast<const uint4*>(xq);
-    for (int i = threadIdx.x; i < M * G; i += blockDim.x) xq_l[i] = xq4[i];
-    for (int i = threadIdx.x; i < M * G; i += blockDim.x) xs_l[i] = bf16_to_f32(xs[i]);
-    __syncthreads();
-
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int n_begin = (blockIdx.x * kGemvWaves + wave) * rows_per_wave;
     const int n_end = min(N, n_begin + rows_per_wave);
 
-    for (int n0 = n_begin; n0 < n_end; n0 += kGemvRowsPerIter) {
-        float acc[kGemvRowsPerIter][M];
+    if constexpr (GPL > 0) {
+        using Chunk = GemvChunk<R, GPL>;
+        auto load = [&](int n0, Chunk& c) {
 #pragma unroll
-        for (int r = 0; r < kGemvRowsPerIter; ++r)
+            for (int r = 0; r < R; ++r) {
+                const int n = max(0, min(n0 + r, n_end - 1));   // clamp: duplicate rows are never stored
+                const uint8_t* wrow = wq + (size_t)n * K2;
+                const uint16_t* srow = ws + (size_t)n * G;
 #pragma unroll
-            for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
-
-        for (int g = lane; g < G; g += 64) {
-            uint4 wv[kGemvRowsPerIter];
-            float swv[kGemvRowsPerIter];
-#pragma unroll
-            for (int r = 0; r < kGemvRowsPerIter; ++r) {
-                const int n = min(n0 + r, n_end - 1);   // duplicate the last row, never store it
-                wv[r] = load_nt16(wq + (size_t)n * K2 + (size_t)g * 16);
-                swv[r] = bf16_to_f32(ws[(size_t)n * G + g]);
-            }
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const uint4 xv = xq_l[m * G + g];
-                const float sxv = xs_l[m * G + g];
-#pragma unroll
-                for (int r = 0; r < kGemvRowsPerIter; ++r) {
-                    const int d = dot32_s4(wv[r], xv);
-                    acc[r][m] = __builtin_fmaf((float)d, sxv * swv[r], acc[r][m]);
+                for (int t = 0; t < GPL; ++t) {
+                    c.w[r][t] = load_nt16(wrow + (size_t)(lane + 64 * t) * 16);
+                    c.s[r][t] = srow[lane + 64 * t];
                 }
             }
+        };
+        Chunk cur, nxt;
+        if (n_begin < n_end) load(n_begin, cur);
+
+        const uint4* xq4 = reinterpret_cast<const uint4*>(xq);
+        for (int i = threadIdx.x; i < M * G; i += blockDim.x) xq_l[i] = xq4[i];
+        for (int i = threadIdx.x; i < M * G; i += blockDim.x) xs_l[i] = bf16_to_f32(xs[i]);
+        __syncthreads();
+
+        for (int n0 = n_begin; n0 < n_end; n0 += R) {
+            const bool more = n0 + R < n_end;
+            if (more) load(n0 + R, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            float acc[R][M];
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < GPL; ++t) {
+                const int g = lane + 64 * t;
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const uint4 xv = xq_l[m * G + g];
+                    const float sxv = xs_l[m * G + g];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const int d = dot32_s4(cur.w[r][t], xv);
+                        acc[r][m] = __builtin_fmaf((float)d, sxv * bf16_to_f32(cur.s[r][t]), acc[r][m]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float v = wave_sum(acc[r][m]);
+                    if (lane == 0 && n0 + r < n_end) y[(size_t)m * N + n0 + r] = f32_to_f16_bits(v);
+                }
+            }
+            if (more) cur = nxt;
         }
+    } else {
+        const uint4* xq4 = reinterpret_cast<const uint4*>(xq);
+        for (int i = threadIdx.x; i < M * G; i += blockDim.x) xq_l[i] = xq4[i];
+        for (int i = threadIdx.x; i < M * G; i += blockDim.x) xs_l[i] = bf16_to_f32(xs[i]);
+        __syncthreads();
+        for (int n0 = n_begin; n0 < n_end; n0 += R) {
+            float acc[R][M];
 #pragma unroll
-        for (int r = 0; r < kGemvRowsPerIter; ++r) {
+            for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const float v = wave_sum(acc[r][m]);
-                if (lane == 0 && n0 + r < n_end) y[(size_t)m * N + n0 + r] = f32_to_f16_bits(v);
+                for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+            for (int g = lane; g < G; g += 64) {
+                uint4 wv[R];
+                float swv[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int n = min(n0 + r, n_end - 1);
+                    wv[r] = load_nt16(wq + (size_t)n * K2 + (size_t)g * 16);
+                    swv[r] = bf16_to_f32(ws[(size_t)n * G + g]);
+                }
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const uint4 xv = xq_l[m * G + g];
+                    const float sxv = xs_l[m * G + g];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const int d = dot32_s4(wv[r], xv);
+                        acc[r][m] = __builtin_fmaf((float)d, sxv * swv[r], acc[r][m]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float v = wave_sum(acc[r][m]);
+                    if (lane == 0 && n0 + r < n_end) y[(size_t)m * N + n0 + r] = f32_to_f16_bits(v);
+                }
             }
         }
     }
 }
 
-template <int M>
+template <int M, int R, int GPL>
+static void launch_gemv_t(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
+                          uint16_t* y, int N, int K, hipStream_t stream) {
+    const int G = K / 32;
+    const size_t smem = (size_t)M * (K / 2) + (size_t)M * G * sizeof(float);
+    // Spread the rows evenly over the wavefronts that are resident at once
+    // (occupancy from the kernel's register and LDS use), so every CU
+    // finishes together.
+    static int resident_waves = 0;
+    if (resident_waves == 0) {
+        int per_cu = 0;
+        int dev = 0, cus = 256;
+        if (hipGetDevice(&dev) == hipSuccess)
+            (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_int4_kernel<M, R, GPL>, 64 * kGemvWaves,
+                                                         smem) != hipSuccess || per_cu < 1)
+            per_cu = 2;
+        resident_waves = per_cu * kGemvWaves * cus;
+    }
+    int rows_per_wave = (N + resident_waves - 1) / resident_waves;
+    rows_per_wave = max(rows_per_wave, 1);
+    const int blocks = (N + kGemvWaves * rows_per_wave - 1) / (kGemvWaves * rows_per_wave);
+    gemv_int4_kernel<M, R, GPL><<<dim3(blocks), dim3(64 * kGemvWaves), smem, stream>>>(xq, xs, wq, ws, y, N, K,
+                                                                                        rows_per_wave);
+}
+
+template <int M, int R>
 static void launch_gemv(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                         uint16_t* y, int N, int K, hipStream_t stream) {
     const int G = K / 32;
-    const size_t smem = (size_t)M * (K / 2) + (size_t)M * G * sizeof(float);
-    // Rows per wavefront: enough workgroups to cover the 256 CUs several times.
-    int rows_per_wave = 8;
-    while (rows_per_wave > 2 && (N + kGemvWaves * rows_per_wave - 1) / (kGemvWaves * rows_per_wave) < 1024)
-        rows_per_wave >>= 1;
-    const int blocks = (N + kGemvWaves * rows_per_wave - 1) / (kGemvWaves * rows_per_wave);
-    gemv_int4_kernel<M><<<blocks, 64 * kGemvWaves, smem, stream>>>(xq, xs, wq, ws, y, N, K, rows_per_wave);
+    if (G == 128)
+        launch_gemv_t<M, R, 2>(xq, xs, wq, ws, y, N, K, stream);
+    else if (G == 256)
+        launch_gemv_t<M, R, 4>(xq, xs, wq, ws, y, N, K, stream);
+    else
+        launch_gemv_t<M, R, 0>(xq, xs, wq, ws, y, N, K, stream);
 }
 
 }  // namespace wush
@@ -123,14 +216,14 @@ extern "C" int wush_gemv_int4(const uint8_t* xq, const uint16_t* xs, const uint8
     WUSH_REQUIRE((size_t)M * (K / 2) + (size_t)M * (K / 32) * 4 <= 64 * 1024);
     const int n = (int)N, k = (int)K;
     switch (M) {
-        case 1: wush::launch_gemv<1>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 2: wush::launch_gemv<2>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 3: wush::launch_gemv<3>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 4: wush::launch_gemv<4>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 5: wush::launch_gemv<5>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 6: wush::launch_gemv<6>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 7: wush::launch_gemv<7>(xq, xs, wq, ws, y, n, k, stream); break;
-        default: wush::launch_gemv<8>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 1: wush::launch_gemv<1, 4>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 2: wush::launch_gemv<2, 4>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 3: wush::launch_gemv<3, 2>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 4: wush::launch_gemv<4, 2>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 5: wush::launch_gemv<5, 1>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 6: wush::launch_gemv<6, 1>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 7: wush::launch_gemv<7, 1>(xq, xs, wq, ws, y, n, k, stream); break;
+        default: wush::launch_gemv<8, 1>(xq, xs, wq, ws, y, n, k, stream); break;
     }
     return (int)hipGetLastError();
 }
