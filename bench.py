@@ -91,8 +91,8 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU: the W4A4 layer path has no "
-                          "multi-GPU mode (see DESIGN.md for how it would shard along N); "
-                          "run with --gpus 1"}))
+                          "multi-GPU mode (it would shard the weight rows along N, column-"
+                          "parallel, with one all-gather of y); run with --gpus 1"}))
         sys.exit(2)
 
     import torch
