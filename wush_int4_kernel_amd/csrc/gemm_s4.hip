@@ -333,19 +333,23 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
     if (nb0 * 32 >= N) return;
 
     // Per-lane base pointers; out-of-range rows are clamped to valid rows and
-    // their data masked, so the streaming loop has no branches.
-    const uint8_t* wp[NB][4];
-    uint32_t wmask[NB][4];
+    // their data masked, so the streaming loop has no branches.  The four
+    // 8-row slices of a 32-row block are one base plus j*8 rows.
+    const uint8_t* wp[NB];
+    uint32_t wmask[NB];
     const uint16_t* sp[NB];
     uint32_t smask[NB];
+    const size_t slice = (size_t)8 * K2;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
+        const int n_first = (nb0 + b) * 32 + (lane >> 3);
+        const int nvalid = N - (nb0 + b) * 32;            // rows of this block that exist
+        uint32_t m = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = (nb0 + b) * 32 + 8 * j + (lane >> 3);
-            wmask[b][j] = n < N ? 0xffffffffu : 0u;
-            wp[b][j] = wq + (size_t)(n < N ? n : N - 1) * K2 + (size_t)(g_begin + (lane & 7)) * 16;
-        }
+        for (int j = 0; j < 4; ++j) m |= (8 * j + (lane >> 3) < nvalid ? 1u : 0u) << j;
+        wmask[b] = m;
+        const int nc = n_first < N ? n_first : N - 1;
+        wp[b] = wq + (size_t)nc * K2 + (size_t)(g_begin + (lane & 7)) * 16;
         const int n = (nb0 + b) * 32 + l32;
         smask[b] = n < N ? 0xffffffffu : 0u;
         sp[b] = ws + (size_t)(n < N ? n : N - 1) * G + g_begin;
@@ -365,7 +369,11 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) S.w[b][j] = load_nt16(wp[b][j] + off);
+            for (int j = 0; j < 4; ++j) {
+                // rows past N re-read the last valid slice (masked below)
+                const size_t row_off = ((wmask[b] >> j) & 1u) ? (size_t)j * slice : 0;
+                S.w[b][j] = load_nt16(wp[b] + row_off + off);
+            }
             S.sw[b] = *reinterpret_cast<const uint4*>(sp[b] + st * kStreamSG);
         }
 #pragma unroll
@@ -379,53 +387,49 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint4 v = S.w[b][j];
+                const uint32_t mk = ((wmask[b] >> j) & 1u) ? 0xffffffffu : 0u;
                 const int row = 8 * j + (lane >> 3), g = lane & 7;
                 uint8_t* base = slab + b * (kStreamSG * 2 * kStreamPlane) + row * 8;
-                *reinterpret_cast<uint2*>(base + (g * 2 + 0) * kStreamPlane) =
-                    make_uint2(v.x & wmask[b][j], v.y & wmask[b][j]);
-                *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) =
-                    make_uint2(v.z & wmask[b][j], v.w & wmask[b][j]);
+                *reinterpret_cast<uint2*>(base + (g * 2 + 0) * kStreamPlane) = make_uint2(v.x & mk, v.y & mk);
+                *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) = make_uint2(v.z & mk, v.w & mk);
             }
         }
-        // 2. activation operands of the 8 groups
-        v4i A[kStreamSG];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            uint4 v = S.x[t];
-            v.x &= xmask; v.y &= xmask; v.z &= xmask; v.w &= xmask;
-            swap_halves(v);
-            uint32_t a0, a1, a2, a3, a4, a5, a6, a7;
-            unpack_s4x8_x16(v.x, a0, a1);
-            unpack_s4x8_x16(v.y, a2, a3);
-            unpack_s4x8_x16(v.z, a4, a5);
-            unpack_s4x8_x16(v.w, a6, a7);
-            A[2 * t] = (v4i){(int)a0, (int)a1, (int)a2, (int)a3};
-            A[2 * t + 1] = (v4i){(int)a4, (int)a5, (int)a6, (int)a7};
-        }
-        // 3. per group: weight fragment from the slab, MFMA, fold
+        // 2. per group pair: activation operands (swap + unpack just in time),
+        //    weight fragment from the slab, MFMA, fold
         const int gi0 = st * kStreamSG;
 #pragma unroll
-        for (int g = 0; g < kStreamSG; ++g) {
-            float sxv[NR];
+        for (int t = 0; t < kStreamSG / 2; ++t) {
+            uint4 xv = S.x[t];
+            xv.x &= xmask; xv.y &= xmask; xv.z &= xmask; xv.w &= xmask;
+            swap_halves(xv);
 #pragma unroll
-            for (int jb = 0; jb < NR / 4; ++jb) {
-                const float4 u = *reinterpret_cast<const float4*>(sx_l + (gi0 + g) * 32 + 8 * jb + 4 * half);
-                sxv[jb * 4 + 0] = u.x; sxv[jb * 4 + 1] = u.y; sxv[jb * 4 + 2] = u.z; sxv[jb * 4 + 3] = u.w;
-            }
+            for (int e = 0; e < 2; ++e) {
+                const int g = 2 * t + e;
+                uint32_t a0, a1, a2, a3;
+                unpack_s4x8_x16(e ? xv.z : xv.x, a0, a1);
+                unpack_s4x8_x16(e ? xv.w : xv.y, a2, a3);
+                const v4i A = {(int)a0, (int)a1, (int)a2, (int)a3};
+                float sxv[NR];
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const uint2 w = *reinterpret_cast<const uint2*>(
-                    slab + b * (kStreamSG * 2 * kStreamPlane) + (g * 2 + half) * kStreamPlane + l32 * 8);
-                uint32_t b0, b1, b2, b3;
-                unpack_s4x8_x16(w.x, b0, b1);
-                unpack_s4x8_x16(w.y, b2, b3);
-                const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
-                const uint32_t sw2 = (&S.sw[b].x)[g >> 1] & smask[b];
-                const float swv = (g & 1) ? __uint_as_float(sw2 & 0xffff0000u) : bf16_to_f32(sw2 & 0xffffu);
-                const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[g], B, (v16i){0}, 0, 0, 0);
+                for (int jb = 0; jb < NR / 4; ++jb) {
+                    const float4 u = *reinterpret_cast<const float4*>(sx_l + (gi0 + g) * 32 + 8 * jb + 4 * half);
+                    sxv[jb * 4 + 0] = u.x; sxv[jb * 4 + 1] = u.y; sxv[jb * 4 + 2] = u.z; sxv[jb * 4 + 3] = u.w;
+                }
 #pragma unroll
-                for (int j = 0; j < NR; ++j)
-                    acc[b][j] = __builtin_fmaf((float)d[j], sxv[j] * swv, acc[b][j]);
+                for (int b = 0; b < NB; ++b) {
+                    const uint2 w = *reinterpret_cast<const uint2*>(
+                        slab + b * (kStreamSG * 2 * kStreamPlane) + (g * 2 + half) * kStreamPlane + l32 * 8);
+                    uint32_t b0, b1, b2, b3;
+                    unpack_s4x8_x16(w.x, b0, b1);
+                    unpack_s4x8_x16(w.y, b2, b3);
+                    const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
+                    const uint32_t sw2 = (&S.sw[b].x)[g >> 1] & smask[b];
+                    const float swv = (g & 1) ? __uint_as_float(sw2 & 0xffff0000u) : bf16_to_f32(sw2 & 0xffffu);
+                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (v16i){0}, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < NR; ++j)
+                        acc[b][j] = __builtin_fmaf((float)d[j], sxv[j] * swv, acc[b][j]);
+                }
             }
         }
     };
@@ -514,6 +518,9 @@ struct Plan {
 #ifndef WUSH_STREAM_PF
 #define WUSH_STREAM_PF 2
 #endif
+#ifndef WUSH_STREAM_WAVES
+#define WUSH_STREAM_WAVES 1024   // split K until this many wavefronts stream (measured best)
+#endif
 constexpr int kStreamNB = 1;
 constexpr int kStreamPF = WUSH_STREAM_PF;        // stages of loads in flight per wavefront
 constexpr size_t kStreamLdsMax = 64 * 1024;
@@ -532,7 +539,7 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         p.mr = (int)((M + 7) / 8 * 8);
         const int64_t waves = (N + 32 * kStreamNB - 1) / (32 * kStreamNB);
         int s = 1;
-        while (s < 16 && waves * s < 2048 && G0 / (2 * s) >= 4 * kStreamSG) s *= 2;
+        while (s < 16 && waves * s < WUSH_STREAM_WAVES && G0 / (2 * s) >= 4 * kStreamSG) s *= 2;
         int64_t gps = (G0 + s - 1) / s;
         gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
         while (stream_smem(gps) > kStreamLdsMax && gps > kStreamSG) {

@@ -9,8 +9,8 @@
 // instruction of a wavefront reads 1 KiB of contiguous codes (16 B per lane)
 // and 128 B of contiguous scales.  The group dot is 4 v_dot8_i32_i4 on the
 // packed nibbles as stored (element 2k low nibble pairs with element 2k low
-// nibble), the fold is one cvt + one mul + one fma in fp32, and a wavefront
-// reduction finishes each output.  Two weight rows are in flight per
+// nibble), the fold is one cvt + one mul + one fma in fp32, and a DPP
+// wavefront reduction (VALU only) finishes each output.  Two weight rows are in flight per
 // wavefront so that each lane keeps 2 x (K/2048) 16-byte loads outstanding.
 #include "wush_device.h"
 #include "../../include/wush_int4.h"
@@ -18,12 +18,9 @@
 namespace wush {
 
 constexpr int kGemvWaves = 4;
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
+#ifndef WUSH_GEMV_R1
+#define WUSH_GEMV_R1 1          // weight rows per chunk at M = 1 (measured best)
+#endif
 
 __device__ __forceinline__ int dot32_s4(const uint4& a, const uint4& b) {
     int d = __builtin_amdgcn_sdot8((int)a.x, (int)b.x, 0, false);
@@ -114,7 +111,7 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const uint8_t* __restric
             for (int r = 0; r < R; ++r) {
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    const float v = wave_sum(acc[r][m]);
+                    const float v = wave_sum_dpp(acc[r][m]);
                     if (lane == 0 && n0 + r < n_end) y[(size_t)m * N + n0 + r] = f32_to_f16_bits(v);
                 }
             }
@@ -155,7 +152,7 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const uint8_t* __restric
             for (int r = 0; r < R; ++r) {
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    const float v = wave_sum(acc[r][m]);
+                    const float v = wave_sum_dpp(acc[r][m]);
                     if (lane == 0 && n0 + r < n_end) y[(size_t)m * N + n0 + r] = f32_to_f16_bits(v);
                 }
             }
@@ -216,7 +213,7 @@ extern "C" int wush_gemv_int4(const uint8_t* xq, const uint16_t* xs, const uint8
     WUSH_REQUIRE((size_t)M * (K / 2) + (size_t)M * (K / 32) * 4 <= 64 * 1024);
     const int n = (int)N, k = (int)K;
     switch (M) {
-        case 1: wush::launch_gemv<1, 4>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 1: wush::launch_gemv<1, WUSH_GEMV_R1>(xq, xs, wq, ws, y, n, k, stream); break;
         case 2: wush::launch_gemv<2, 4>(xq, xs, wq, ws, y, n, k, stream); break;
         case 3: wush::launch_gemv<3, 2>(xq, xs, wq, ws, y, n, k, stream); break;
         case 4: wush::launch_gemv<4, 2>(xq, xs, wq, ws, y, n, k, stream); break;

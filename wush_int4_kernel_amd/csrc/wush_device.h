@@ -86,6 +86,25 @@ __device__ __forceinline__ uint32_t quant_group32(const float (&v)[32], uint32_t
     return sb;
 }
 
+// Sum over the 64 lanes of a wavefront on the VALU (DPP), result returned
+// to every lane: quad_perm swaps and row mirrors reduce each 16-lane row,
+// row_bcast:15 / row_bcast:31 fold rows 0-2 into row 3, lane 63 holds the
+// total.  Lanes whose DPP source is masked add 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = dpp_add<0xB1, 0xf>(v);    // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xf>(v);    // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xf>(v);   // row_half_mirror
+    v = dpp_add<0x140, 0xf>(v);   // row_mirror: every lane holds its row's sum
+    v = dpp_add<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte streaming load with the non-temporal hint (weights are read once).
