@@ -299,7 +299,7 @@ struct StreamStage {
     uint4 sw[NB];       // 8 bf16 weight scales of this lane's column
 };
 
-template <int MR, int NB, int PF>
+template <int MR, int NB, int PF, bool XLDS>
 __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __restrict__ xq,
                                                              const uint16_t* __restrict__ xs,
                                                              const uint8_t* __restrict__ wq,
@@ -309,7 +309,9 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
                                                              int M, int N, int K, int groups_per_split) {
     constexpr int NR = MR / 2;
     constexpr int kSlab = NB * kStreamSG * 2 * kStreamPlane;    // bytes of one wavefront's slab
+    constexpr int XR = XLDS ? 8 : 32;            // activation rows staged per group
     static_assert(MR % 8 == 0 && MR <= 32, "fold rows");
+    static_assert(!XLDS || MR == 8, "LDS-resident activations only for M <= 8");
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -320,12 +322,25 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
     const int g_begin = blockIdx.y * groups_per_split;
     const int g_end = min(G, g_begin + groups_per_split);
     const int gcount = g_end - g_begin;          // multiple of kStreamSG
-    float* sx_l = reinterpret_cast<float*>(smem);                       // [gcount][32]
-    uint8_t* slab = smem + (size_t)groups_per_split * 32 * sizeof(float) + (size_t)wave * kSlab;
+    float* sx_l = reinterpret_cast<float*>(smem);                       // [gcount][XR]
+    uint8_t* x_l = smem + (size_t)groups_per_split * XR * sizeof(float); // XLDS: [gcount][2][8][8 B]
+    uint8_t* x_zero = x_l + (XLDS ? (size_t)groups_per_split * 128 : 0);   // XLDS: 16 zero bytes
+    uint8_t* slab = x_zero + (XLDS ? 16 : 0) + (size_t)wave * kSlab;
 
-    for (int i = threadIdx.x; i < gcount * 32; i += 256) {
-        const int g = i >> 5, m = i & 31;
+    for (int i = threadIdx.x; i < gcount * XR; i += 256) {
+        const int g = i / XR, m = i % XR;
         sx_l[i] = (m < M) ? bf16_to_f32(xs[(size_t)m * G + g_begin + g]) : 0.0f;
+    }
+    if constexpr (XLDS) {
+        if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(x_zero)[threadIdx.x] = 0u;
+        // activation codes of the slice, fragment-major [group][k-half][row][8 B]
+        for (int i = threadIdx.x; i < gcount * 8; i += 256) {
+            const int g = i >> 3, m = i & 7;
+            const uint4 v = (m < M) ? *reinterpret_cast<const uint4*>(xq + (size_t)m * K2 + (size_t)(g_begin + g) * 16)
+                                    : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint2*>(x_l + (size_t)g * 128 + m * 8) = make_uint2(v.x, v.y);
+            *reinterpret_cast<uint2*>(x_l + (size_t)g * 128 + 64 + m * 8) = make_uint2(v.z, v.w);
+        }
     }
     __syncthreads();
 
@@ -338,7 +353,6 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
     const uint8_t* wp[NB];
     uint32_t wmask[NB];
     const uint16_t* sp[NB];
-    uint32_t smask[NB];
     const size_t slice = (size_t)8 * K2;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -351,11 +365,13 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
         const int nc = n_first < N ? n_first : N - 1;
         wp[b] = wq + (size_t)nc * K2 + (size_t)(g_begin + (lane & 7)) * 16;
         const int n = (nb0 + b) * 32 + l32;
-        smask[b] = n < N ? 0xffffffffu : 0u;
         sp[b] = ws + (size_t)(n < N ? n : N - 1) * G + g_begin;
     }
-    const uint32_t xmask = l32 < M ? 0xffffffffu : 0u;
     const uint8_t* xp = xq + (size_t)(l32 < M ? l32 : 0) * K2 + (size_t)(g_begin + half) * 16;
+    // LDS-resident activations: lanes of MFMA rows 8..31 read an 8-byte zero
+    // word (stride 0) instead of masking every group
+    const uint8_t* x_rd = l32 < 8 ? x_l + half * 64 + l32 * 8 : x_zero;
+    const int x_gstride = l32 < 8 ? 128 : 0;
 
     float acc[NB][NR];
 #pragma unroll
@@ -370,14 +386,17 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
         for (int b = 0; b < NB; ++b) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                // rows past N re-read the last valid slice (masked below)
+                // rows past N re-read the block's first valid rows; they only
+                // feed output columns >= N, which are never stored
                 const size_t row_off = ((wmask[b] >> j) & 1u) ? (size_t)j * slice : 0;
                 S.w[b][j] = load_nt16(wp[b] + row_off + off);
             }
             S.sw[b] = *reinterpret_cast<const uint4*>(sp[b] + st * kStreamSG);
         }
+        if constexpr (!XLDS) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) S.x[t] = *reinterpret_cast<const uint4*>(xp + off + (size_t)t * 32);
+            for (int t = 0; t < 4; ++t) S.x[t] = *reinterpret_cast<const uint4*>(xp + off + (size_t)t * 32);
+        }
     };
 
     auto process = [&](int st, StreamStage<NB>& S) {
@@ -387,11 +406,10 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint4 v = S.w[b][j];
-                const uint32_t mk = ((wmask[b] >> j) & 1u) ? 0xffffffffu : 0u;
                 const int row = 8 * j + (lane >> 3), g = lane & 7;
                 uint8_t* base = slab + b * (kStreamSG * 2 * kStreamPlane) + row * 8;
-                *reinterpret_cast<uint2*>(base + (g * 2 + 0) * kStreamPlane) = make_uint2(v.x & mk, v.y & mk);
-                *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) = make_uint2(v.z & mk, v.w & mk);
+                *reinterpret_cast<uint2*>(base + (g * 2 + 0) * kStreamPlane) = make_uint2(v.x, v.y);
+                *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) = make_uint2(v.z, v.w);
             }
         }
         // 2. per group pair: activation operands (swap + unpack just in time),
@@ -399,20 +417,29 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
         const int gi0 = st * kStreamSG;
 #pragma unroll
         for (int t = 0; t < kStreamSG / 2; ++t) {
-            uint4 xv = S.x[t];
-            xv.x &= xmask; xv.y &= xmask; xv.z &= xmask; xv.w &= xmask;
-            swap_halves(xv);
+            uint4 xv = make_uint4(0, 0, 0, 0);
+            if constexpr (!XLDS) {
+                xv = S.x[t];                     // rows >= M duplicate row 0: outputs not stored
+                swap_halves(xv);
+            }
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const int g = 2 * t + e;
                 uint32_t a0, a1, a2, a3;
-                unpack_s4x8_x16(e ? xv.z : xv.x, a0, a1);
-                unpack_s4x8_x16(e ? xv.w : xv.y, a2, a3);
+                if constexpr (XLDS) {
+                    // rows 0-7 of the MFMA come from LDS; rows 8-31 are zero
+                    const uint2 xw = *reinterpret_cast<const uint2*>(x_rd + (size_t)(gi0 + g) * x_gstride);
+                    unpack_s4x8_x16(xw.x, a0, a1);
+                    unpack_s4x8_x16(xw.y, a2, a3);
+                } else {
+                    unpack_s4x8_x16(e ? xv.z : xv.x, a0, a1);
+                    unpack_s4x8_x16(e ? xv.w : xv.y, a2, a3);
+                }
                 const v4i A = {(int)a0, (int)a1, (int)a2, (int)a3};
                 float sxv[NR];
 #pragma unroll
                 for (int jb = 0; jb < NR / 4; ++jb) {
-                    const float4 u = *reinterpret_cast<const float4*>(sx_l + (gi0 + g) * 32 + 8 * jb + 4 * half);
+                    const float4 u = *reinterpret_cast<const float4*>(sx_l + (gi0 + g) * XR + 8 * jb + 4 * half);
                     sxv[jb * 4 + 0] = u.x; sxv[jb * 4 + 1] = u.y; sxv[jb * 4 + 2] = u.z; sxv[jb * 4 + 3] = u.w;
                 }
 #pragma unroll
@@ -423,7 +450,7 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
                     unpack_s4x8_x16(w.x, b0, b1);
                     unpack_s4x8_x16(w.y, b2, b3);
                     const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
-                    const uint32_t sw2 = (&S.sw[b].x)[g >> 1] & smask[b];
+                    const uint32_t sw2 = (&S.sw[b].x)[g >> 1];
                     const float swv = (g & 1) ? __uint_as_float(sw2 & 0xffff0000u) : bf16_to_f32(sw2 & 0xffffu);
                     const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (v16i){0}, 0, 0, 0);
 #pragma unroll
@@ -523,10 +550,16 @@ struct Plan {
 #endif
 constexpr int kStreamNB = 1;
 constexpr int kStreamPF = WUSH_STREAM_PF;        // stages of loads in flight per wavefront
+#ifndef WUSH_STREAM_PFX
+#define WUSH_STREAM_PFX 2
+#endif
+constexpr int kStreamPFX = WUSH_STREAM_PFX;      // same, M <= 8 (activations in LDS)
 constexpr size_t kStreamLdsMax = 64 * 1024;
 
-static size_t stream_smem(int64_t gps) {
-    return (size_t)gps * 32 * sizeof(float) + 4 * (size_t)kStreamNB * kStreamSG * 2 * kStreamPlane;
+static size_t stream_smem(int64_t gps, bool xlds) {
+    const size_t xr = xlds ? 8 : 32;
+    return (size_t)gps * xr * sizeof(float) + (xlds ? (size_t)gps * 128 + 16 : 0) +
+           4 * (size_t)kStreamNB * kStreamSG * 2 * kStreamPlane;
 }
 
 static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available, bool allow_split) {
@@ -542,14 +575,15 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         while (s < 16 && waves * s < WUSH_STREAM_WAVES && G0 / (2 * s) >= 4 * kStreamSG) s *= 2;
         int64_t gps = (G0 + s - 1) / s;
         gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
-        while (stream_smem(gps) > kStreamLdsMax && gps > kStreamSG) {
+        const bool xlds = p.mr == 8;
+        while (stream_smem(gps, xlds) > kStreamLdsMax && gps > kStreamSG) {
             s *= 2;
             gps = (G0 + s - 1) / s;
             gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
         }
         s = (int)((G0 + gps - 1) / gps);
         const bool ws_ok = s == 1 || (size_t)s * (size_t)M * (size_t)N * sizeof(float) <= ws_bytes_available;
-        if (ws_ok && stream_smem(gps) <= kStreamLdsMax) {
+        if (ws_ok && stream_smem(gps, xlds) <= kStreamLdsMax) {
             p.splits = s;
             p.groups_per_split = (int)gps;
             return p;
@@ -606,13 +640,13 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     const int m = (int)M, n = (int)N, k = (int)K;
     if (p.cfg == 3) {
         if constexpr (!PT) {
-            const size_t smem = stream_smem(p.groups_per_split);
+            const size_t smem = stream_smem(p.groups_per_split, p.mr == 8);
             dim3 grid((unsigned)((N + p.tn - 1) / p.tn), (unsigned)p.splits);
             switch (p.mr) {
-                case 8: gemm_s4_stream_kernel<8, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
-                case 16: gemm_s4_stream_kernel<16, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
-                case 24: gemm_s4_stream_kernel<24, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
-                default: gemm_s4_stream_kernel<32, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                case 8: gemm_s4_stream_kernel<8, kStreamNB, kStreamPFX, true><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                case 16: gemm_s4_stream_kernel<16, kStreamNB, kStreamPF, false><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                case 24: gemm_s4_stream_kernel<24, kStreamNB, kStreamPF, false><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                default: gemm_s4_stream_kernel<32, kStreamNB, kStreamPF, false><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
             }
         }
     } else if (p.cfg == 0) {
