@@ -8,9 +8,14 @@
 // v_mfma_i32_32x32x32_i8, so every MFMA produces D of one group for a 32x32
 // block, exact in int32.  The s4 codes are unpacked to int8 in VGPRs as
 // 16*code ((w<<4)&0xF0F0F0F0 and w&0xF0F0F0F0, exact for [-8,7]) so the MFMA
-// returns 256*D; the 2^-8 is applied once at the output.  D is folded into an
-// fp32 accumulator with the fp32 product of the two bf16 group scales
-// (exact: 8-bit x 8-bit significands): acc = fma(float(D), sx*sw, acc).
+// returns 256*D.  D is folded into an fp32 accumulator with the product of the
+// two bf16 group scales: acc = fma(float(D), 2*sx*sw, acc).  The scale
+// products come from a second MFMA, v_mfma_f32_32x32x16_bf16, whose operands
+// hold only the lane's own scale in element 0: both lane halves contribute the
+// same exact bf16 x bf16 product (8-bit x 8-bit significands), so the MFMA
+// returns 2*sx*sw exactly, already in the accumulator layout of D.  The
+// factor 2*256 is removed once at the output (exact power of two), so the
+// result equals the per-element fold fma(float(D), sx*sw, acc) / 256.
 //
 // Workgroup = 4 wavefronts in a WAVES_M x WAVES_N grid, each wavefront owns a
 // (32*BM) x (32*BN) output tile.  K advances 4 groups (64 code bytes per row)
@@ -26,20 +31,38 @@ namespace wush {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Fold factor of every D element, 2*sx[row]*sw[col], for one 32x32 block in
+// the 32x32 MFMA accumulator layout.  sx_bits / sw_bits: bf16 bits (upper 16
+// bits zero) of the scale of row l%32 / column l%32.  Element 0 of the two
+// operands sits at a distinct k in each lane half and every other element is
+// zero, so the MFMA sums exactly two equal exact products.
+__device__ __forceinline__ v16f scale_products(uint32_t sx_bits, uint32_t sw_bits) {
+    const v4i a = {(int)sx_bits, 0, 0, 0};
+    const v4i b = {(int)sw_bits, 0, 0, 0};
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                   (v16f){0.0f}, 0, 0, 0);
+}
+
+// fp32 accumulator -> output: removes the 16*16 of the unpacked codes and the
+// 2 of scale_products.
+constexpr float kFoldOutScale = 1.0f / 512.0f;
 
 constexpr int kPlanePad = 32;                    // bytes of padding per (group, half) plane
 
 // LDS layout of one pipeline buffer: codes fragment-major
 // [group][k-half][row][8 B] (+ padding per plane) so the MFMA operand reads
-// (lane = row, 8 B) are conflict-free, then fp32 scales [group][row].
+// (lane = row, 8 B) are conflict-free, then bf16 scales [group][row].
 template <int TM, int TN, int SG>
 struct GemmSmem {
     static constexpr int kAPlane = TM * 8 + kPlanePad;
     static constexpr int kBPlane = TN * 8 + kPlanePad;
     static constexpr int kACodes = SG * 2 * kAPlane;
     static constexpr int kBCodes = SG * 2 * kBPlane;
-    static constexpr int kAScale = SG * TM * 4;
-    static constexpr int kBScale = SG * TN * 4;
+    static constexpr int kAScale = SG * TM * 2;
+    static constexpr int kBScale = SG * TN * 2;
     static constexpr int kBuf = kACodes + kBCodes + kAScale + kBScale;
     static constexpr int kBytes = 2 * kBuf;
 };
@@ -54,8 +77,8 @@ struct StageRegs {
     static constexpr int kBChunks = (TN * SG + 255) / 256;
     uint4 a[kAChunks];
     uint4 b[kBChunks];
-    float sa[kAChunks];
-    float sb[kBChunks];
+    uint16_t sa[kAChunks];
+    uint16_t sb[kBChunks];
 };
 
 // BM x BN 32x32 blocks per wavefront, WAVES_M x WAVES_N wavefronts, SG groups
@@ -106,7 +129,7 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
             const bool ok = row < TM && gm < M && gg < g_end;
             r.a[c] = ok ? *reinterpret_cast<const uint4*>(xq + (size_t)gm * K2 + (size_t)gg * 16)
                         : make_uint4(0, 0, 0, 0);
-            if constexpr (!PER_TENSOR) r.sa[c] = ok ? bf16_to_f32(xs[(size_t)gm * G + gg]) : 0.0f;
+            if constexpr (!PER_TENSOR) r.sa[c] = ok ? xs[(size_t)gm * G + gg] : (uint16_t)0;
         }
 #pragma unroll
         for (int c = 0; c < R::kBChunks; ++c) {
@@ -116,15 +139,15 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
             const bool ok = row < TN && gn < N && gg < g_end;
             r.b[c] = ok ? *reinterpret_cast<const uint4*>(wq + (size_t)gn * K2 + (size_t)gg * 16)
                         : make_uint4(0, 0, 0, 0);
-            if constexpr (!PER_TENSOR) r.sb[c] = ok ? bf16_to_f32(ws[(size_t)gn * G + gg]) : 0.0f;
+            if constexpr (!PER_TENSOR) r.sb[c] = ok ? ws[(size_t)gn * G + gg] : (uint16_t)0;
         }
     };
 
     auto store_stage = [&](int buf, const R& r) {
         uint8_t* base = smem + buf * S::kBuf;
         uint8_t* bbase = base + S::kACodes;
-        float* sa = reinterpret_cast<float*>(base + S::kACodes + S::kBCodes);
-        float* sbp = sa + SG * TM;
+        uint16_t* sa = reinterpret_cast<uint16_t*>(base + S::kACodes + S::kBCodes);
+        uint16_t* sbp = sa + SG * TM;
 #pragma unroll
         for (int c = 0; c < R::kAChunks; ++c) {
             const int id = tid + c * 256;
@@ -162,8 +185,8 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
     auto compute_stage = [&](int buf, int st) {
         const uint8_t* base = smem + buf * S::kBuf;
         const uint8_t* bbase = base + S::kACodes;
-        const float* sa = reinterpret_cast<const float*>(base + S::kACodes + S::kBCodes);
-        const float* sbp = sa + SG * TM;
+        const uint16_t* sa = reinterpret_cast<const uint16_t*>(base + S::kACodes + S::kBCodes);
+        const uint16_t* sbp = sa + SG * TM;
         const int groups_here = min(SG, g_end - (g_begin + st * SG));
 #pragma unroll
         for (int g = 0; g < SG; ++g) {
@@ -195,29 +218,20 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
                         iacc[bm][bn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[bm], bfr[bn],
                                                                               iacc[bm][bn], 0, 0, 0);
             } else {
-                float swv[BN];
+                uint32_t swb[BN];
 #pragma unroll
-                for (int bn = 0; bn < BN; ++bn) swv[bn] = sbp[g * TN + wn + bn * 32 + l32];
+                for (int bn = 0; bn < BN; ++bn) swb[bn] = sbp[g * TN + wn + bn * 32 + l32];
 #pragma unroll
                 for (int bm = 0; bm < BM; ++bm) {
-                    // rows of this lane: 8*(j/4) + 4*half + (j%4), j = 0..NR-1
-                    float sxv[NR];
-#pragma unroll
-                    for (int jb = 0; jb < NR / 4; ++jb) {
-                        const float4 v = *reinterpret_cast<const float4*>(
-                            sa + g * TM + wm + bm * 32 + jb * 8 + half * 4);
-                        sxv[jb * 4 + 0] = v.x;
-                        sxv[jb * 4 + 1] = v.y;
-                        sxv[jb * 4 + 2] = v.z;
-                        sxv[jb * 4 + 3] = v.w;
-                    }
+                    const uint32_t sxb = sa[g * TM + wm + bm * 32 + l32];
 #pragma unroll
                     for (int bn = 0; bn < BN; ++bn) {
                         const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[bm], bfr[bn],
                                                                              (v16i){0}, 0, 0, 0);
+                        const v16f sc = scale_products(sxb, swb[bn]);
 #pragma unroll
                         for (int j = 0; j < NR; ++j)
-                            acc[bm][bn][j] = __builtin_fmaf((float)d[j], sxv[j] * swv[bn], acc[bm][bn][j]);
+                            acc[bm][bn][j] = __builtin_fmaf((float)d[j], sc[j], acc[bm][bn][j]);
                     }
                 }
             }
@@ -238,8 +252,9 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
         }
     }
 
-    // Epilogue.  The MFMA ran on 16*code operands: scale by 2^-8.
-    float out_scale = 1.0f / 256.0f;
+    // Epilogue.  The MFMA ran on 16*code operands (2^-8); the group-scaled
+    // fold also carries the 2 of scale_products.
+    float out_scale = kFoldOutScale;
     if constexpr (PER_TENSOR) out_scale = (alpha_dev ? *alpha_dev : alpha) * (1.0f / 256.0f);
 #pragma unroll
     for (int bm = 0; bm < BM; ++bm)
@@ -275,9 +290,10 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
 // transposing writes and the fragment reads bank-conflict-free, and no
 // workgroup barrier is needed.  Activations (<= 32 rows, L2-resident) are
 // loaded as whole 16-byte groups and re-paired across lane halves with
-// v_permlane32_swap.  Weight scales arrive as one 16-byte load per row and
-// stage; x scales for the slice sit in LDS.  Requires K % 256 == 0 and slices
-// of whole stages.
+// v_permlane32_swap; at M <= 8 (XLDS) the slice's activation codes are staged
+// once in LDS instead.  Weight scales arrive as one 16-byte load per row and
+// stage; the bf16 x scales of the slice sit in LDS.  Requires K % 256 == 0
+// and slices of whole stages.
 constexpr int kStreamSG = 8;                     // groups per stage
 constexpr int kStreamPlane = 32 * 8 + 16;        // bytes per (group, half) plane of a 32-row block
 
@@ -322,17 +338,15 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
     const int g_begin = blockIdx.y * groups_per_split;
     const int g_end = min(G, g_begin + groups_per_split);
     const int gcount = g_end - g_begin;          // multiple of kStreamSG
-    float* sx_l = reinterpret_cast<float*>(smem);                       // [gcount][XR]
-    uint8_t* x_l = smem + (size_t)groups_per_split * XR * sizeof(float); // XLDS: [gcount][2][8][8 B]
-    uint8_t* x_zero = x_l + (XLDS ? (size_t)groups_per_split * 128 : 0);   // XLDS: 16 zero bytes
-    uint8_t* slab = x_zero + (XLDS ? 16 : 0) + (size_t)wave * kSlab;
+    uint16_t* sx_l = reinterpret_cast<uint16_t*>(smem);                    // bf16 [gcount][XR]
+    uint8_t* x_l = smem + (size_t)groups_per_split * XR * sizeof(uint16_t); // XLDS: [gcount][2][8][8 B]
+    uint8_t* slab = x_l + (XLDS ? (size_t)groups_per_split * 128 : 0) + (size_t)wave * kSlab;
 
     for (int i = threadIdx.x; i < gcount * XR; i += 256) {
         const int g = i / XR, m = i % XR;
-        sx_l[i] = (m < M) ? bf16_to_f32(xs[(size_t)m * G + g_begin + g]) : 0.0f;
+        sx_l[i] = (m < M) ? xs[(size_t)m * G + g_begin + g] : (uint16_t)0;
     }
     if constexpr (XLDS) {
-        if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(x_zero)[threadIdx.x] = 0u;
         // activation codes of the slice, fragment-major [group][k-half][row][8 B]
         for (int i = threadIdx.x; i < gcount * 8; i += 256) {
             const int g = i >> 3, m = i & 7;
@@ -368,10 +382,10 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
         sp[b] = ws + (size_t)(n < N ? n : N - 1) * G + g_begin;
     }
     const uint8_t* xp = xq + (size_t)(l32 < M ? l32 : 0) * K2 + (size_t)(g_begin + half) * 16;
-    // LDS-resident activations: lanes of MFMA rows 8..31 read an 8-byte zero
-    // word (stride 0) instead of masking every group
-    const uint8_t* x_rd = l32 < 8 ? x_l + half * 64 + l32 * 8 : x_zero;
-    const int x_gstride = l32 < 8 ? 128 : 0;
+    // LDS-resident activations (MR == 8): MFMA rows 8..31 repeat rows 0..7;
+    // only accumulator rows 0..7 are folded, so their content is irrelevant
+    const uint8_t* x_rd = x_l + half * 64 + (l32 & 7) * 8;
+    const int sx_row = XLDS ? (l32 & 7) : l32;
 
     float acc[NB][NR];
 #pragma unroll
@@ -427,8 +441,7 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
                 const int g = 2 * t + e;
                 uint32_t a0, a1, a2, a3;
                 if constexpr (XLDS) {
-                    // rows 0-7 of the MFMA come from LDS; rows 8-31 are zero
-                    const uint2 xw = *reinterpret_cast<const uint2*>(x_rd + (size_t)(gi0 + g) * x_gstride);
+                    const uint2 xw = *reinterpret_cast<const uint2*>(x_rd + (size_t)(gi0 + g) * 128);
                     unpack_s4x8_x16(xw.x, a0, a1);
                     unpack_s4x8_x16(xw.y, a2, a3);
                 } else {
@@ -436,12 +449,7 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
                     unpack_s4x8_x16(e ? xv.w : xv.y, a2, a3);
                 }
                 const v4i A = {(int)a0, (int)a1, (int)a2, (int)a3};
-                float sxv[NR];
-#pragma unroll
-                for (int jb = 0; jb < NR / 4; ++jb) {
-                    const float4 u = *reinterpret_cast<const float4*>(sx_l + (gi0 + g) * XR + 8 * jb + 4 * half);
-                    sxv[jb * 4 + 0] = u.x; sxv[jb * 4 + 1] = u.y; sxv[jb * 4 + 2] = u.z; sxv[jb * 4 + 3] = u.w;
-                }
+                const uint32_t sxb = sx_l[(gi0 + g) * XR + sx_row];
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
                     const uint2 w = *reinterpret_cast<const uint2*>(
@@ -451,11 +459,12 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
                     unpack_s4x8_x16(w.y, b2, b3);
                     const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
                     const uint32_t sw2 = (&S.sw[b].x)[g >> 1];
-                    const float swv = (g & 1) ? __uint_as_float(sw2 & 0xffff0000u) : bf16_to_f32(sw2 & 0xffffu);
+                    const uint32_t swb = (g & 1) ? (sw2 >> 16) : (sw2 & 0xffffu);
                     const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (v16i){0}, 0, 0, 0);
+                    const v16f sc = scale_products(sxb, swb);
 #pragma unroll
                     for (int j = 0; j < NR; ++j)
-                        acc[b][j] = __builtin_fmaf((float)d[j], sxv[j] * swv, acc[b][j]);
+                        acc[b][j] = __builtin_fmaf((float)d[j], sc[j], acc[b][j]);
                 }
             }
         }
@@ -485,7 +494,7 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
         for (int j = 0; j < NR; ++j) {
             const int row = 8 * (j >> 2) + 4 * half + (j & 3);
             if (row < M) {
-                const float v = acc[b][j] * (1.0f / 256.0f);
+                const float v = acc[b][j] * kFoldOutScale;
                 if (partial != nullptr)
                     partial[((size_t)blockIdx.y * M + row) * N + col] = v;
                 else
@@ -548,7 +557,10 @@ struct Plan {
 #ifndef WUSH_STREAM_WAVES
 #define WUSH_STREAM_WAVES 1024   // split K until this many wavefronts stream (measured best)
 #endif
-constexpr int kStreamNB = 1;
+#ifndef WUSH_STREAM_NB
+#define WUSH_STREAM_NB 1
+#endif
+constexpr int kStreamNB = WUSH_STREAM_NB;      // 32-row weight blocks per wavefront
 constexpr int kStreamPF = WUSH_STREAM_PF;        // stages of loads in flight per wavefront
 #ifndef WUSH_STREAM_PFX
 #define WUSH_STREAM_PFX 2
@@ -558,7 +570,7 @@ constexpr size_t kStreamLdsMax = 64 * 1024;
 
 static size_t stream_smem(int64_t gps, bool xlds) {
     const size_t xr = xlds ? 8 : 32;
-    return (size_t)gps * xr * sizeof(float) + (xlds ? (size_t)gps * 128 + 16 : 0) +
+    return (size_t)gps * xr * sizeof(uint16_t) + (xlds ? (size_t)gps * 128 : 0) +
            4 * (size_t)kStreamNB * kStreamSG * 2 * kStreamPlane;
 }
 
