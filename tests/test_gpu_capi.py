@@ -277,6 +277,32 @@ def test_gemm_group_dots_exact_per_group(capi):
             assert np.array_equal(y, D[: y.shape[0], :, gg].astype(np.float64)), (kernel, gg)
 
 
+@pytest.mark.parametrize("M", [1, 8, 17, 32])
+def test_gemm_scale_alignment_paths_agree(capi, M):
+    # Scales that are only 2-byte aligned take the LDS-tiled kernel, 16-byte
+    # aligned ones the streaming kernel (decode M, K % 256 == 0).  Both fold
+    # the same exact group dots in the same group order: equal bit for bit.
+    import torch
+    g = rng(4250 + M)
+    N, K = 300, 1024
+    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    ref = oracle.gemm_f64(xq, xs, wq, ws)
+    dx, dw = to_dev_u8(xq), to_dev_u8(wq)
+    outs = []
+    for shift in (0, 1):
+        bx = torch.zeros(xs.size + 8, dtype=torch.bfloat16, device="cuda")
+        bw = torch.zeros(ws.size + 8, dtype=torch.bfloat16, device="cuda")
+        bx[shift:shift + xs.size] = to_dev_bf16(xs).reshape(-1)
+        bw[shift:shift + ws.size] = to_dev_bf16(ws).reshape(-1)
+        y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+        capi.gemm_s4(dx.data_ptr(), bx.data_ptr() + 2 * shift, dw.data_ptr(), bw.data_ptr() + 2 * shift,
+                     y.data_ptr(), M, N, K, None, 0, _stream())
+        torch.cuda.synchronize()
+        outs.append(f16_tensor_f64(y))
+        assert rel_fro(outs[-1], ref) < FRO_TOL, (M, shift, rel_fro(outs[-1], ref))
+    assert np.array_equal(outs[0], outs[1])
+
+
 def test_gemm_golden_fixture(capi):
     gm = np.load(os.path.join(GOLDEN, "gemm_small.npz"))
     y = run_gemm(capi, gm["xq"], gm["xs"], gm["wq"], gm["ws"])

@@ -342,24 +342,9 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
     uint8_t* x_l = smem + (size_t)groups_per_split * XR * sizeof(uint16_t); // XLDS: [gcount][2][8][8 B]
     uint8_t* slab = x_l + (XLDS ? (size_t)groups_per_split * 128 : 0) + (size_t)wave * kSlab;
 
-    for (int i = threadIdx.x; i < gcount * XR; i += 256) {
-        const int g = i / XR, m = i % XR;
-        sx_l[i] = (m < M) ? xs[(size_t)m * G + g_begin + g] : (uint16_t)0;
-    }
-    if constexpr (XLDS) {
-        // activation codes of the slice, fragment-major [group][k-half][row][8 B]
-        for (int i = threadIdx.x; i < gcount * 8; i += 256) {
-            const int g = i >> 3, m = i & 7;
-            const uint4 v = (m < M) ? *reinterpret_cast<const uint4*>(xq + (size_t)m * K2 + (size_t)(g_begin + g) * 16)
-                                    : make_uint4(0, 0, 0, 0);
-            *reinterpret_cast<uint2*>(x_l + (size_t)g * 128 + m * 8) = make_uint2(v.x, v.y);
-            *reinterpret_cast<uint2*>(x_l + (size_t)g * 128 + 64 + m * 8) = make_uint2(v.z, v.w);
-        }
-    }
-    __syncthreads();
-
+    // Wavefronts past the last row block (only in the last workgroup) stream
+    // clamped rows and store nothing.
     const int nb0 = (blockIdx.x * 4 + wave) * NB;
-    if (nb0 * 32 >= N) return;
 
     // Per-lane base pointers; out-of-range rows are clamped to valid rows and
     // their data masked, so the streaming loop has no branches.  The four
@@ -413,6 +398,72 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
         }
     };
 
+    // The first stages' weights do not depend on the staged data: request
+    // them before the staging so their HBM latency overlaps it.
+    StreamStage<NB> buf[PF];
+#pragma unroll
+    for (int d = 0; d < PF; ++d) load(min(d, nst - 1), buf[d]);
+
+    // Stage the slice's x scales (and at M <= 8 its activation codes) in LDS.
+    // All of a thread's loads are issued before its LDS stores, so the
+    // staging costs one L2 round trip, not one per element.
+    {
+        // one 16-byte load = the scales of 8 consecutive groups of one row
+        constexpr int U = XR / 8;
+        const int nchunk = XR * (gcount >> 3);
+        for (int c0 = threadIdx.x; c0 < nchunk; c0 += 256 * U) {
+            uint4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + u * 256;
+                const int m = c % XR, gc = c / XR;
+                v[u] = (c < nchunk && m < M)
+                           ? *reinterpret_cast<const uint4*>(xs + (size_t)m * G + g_begin + gc * 8)
+                           : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + u * 256;
+                if (c < nchunk) {
+                    const int m = c % XR, gc = c / XR;
+                    const uint32_t* h = &v[u].x;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        sx_l[(gc * 8 + 2 * e) * XR + m] = (uint16_t)(h[e] & 0xffffu);
+                        sx_l[(gc * 8 + 2 * e + 1) * XR + m] = (uint16_t)(h[e] >> 16);
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (XLDS) {
+        // activation codes of the slice, fragment-major [group][k-half][row][8 B]
+        constexpr int U = 8;
+        const int nchunk = gcount * 8;
+        for (int c0 = threadIdx.x; c0 < nchunk; c0 += 256 * U) {
+            uint4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + u * 256;
+                const int g = c >> 3, m = c & 7;
+                v[u] = (c < nchunk && m < M)
+                           ? *reinterpret_cast<const uint4*>(xq + (size_t)m * K2 + (size_t)(g_begin + g) * 16)
+                           : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + u * 256;
+                if (c < nchunk) {
+                    const int g = c >> 3, m = c & 7;
+                    *reinterpret_cast<uint2*>(x_l + (size_t)g * 128 + m * 8) = make_uint2(v[u].x, v[u].y);
+                    *reinterpret_cast<uint2*>(x_l + (size_t)g * 128 + 64 + m * 8) = make_uint2(v[u].z, v[u].w);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (nb0 * 32 >= N) return;
+
     auto process = [&](int st, StreamStage<NB>& S) {
         // 1. transpose this stage's weights into the slab
 #pragma unroll
@@ -426,53 +477,63 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
                 *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) = make_uint2(v.z, v.w);
             }
         }
-        // 2. per group pair: activation operands (swap + unpack just in time),
-        //    weight fragment from the slab, MFMA, fold
+        // 2. per group: activation operand, weight fragment from the slab, the
+        //    two MFMAs (D and the scale products), then the fold.  Software
+        //    pipelined: the MFMAs of group g+1 are issued before the fold of
+        //    group g, so the fold overlaps the MFMA latency of the next group.
         const int gi0 = st * kStreamSG;
+        uint4 xv[kStreamSG / 2];
+        if constexpr (!XLDS) {
 #pragma unroll
-        for (int t = 0; t < kStreamSG / 2; ++t) {
-            uint4 xv = make_uint4(0, 0, 0, 0);
-            if constexpr (!XLDS) {
-                xv = S.x[t];                     // rows >= M duplicate row 0: outputs not stored
-                swap_halves(xv);
+            for (int t = 0; t < kStreamSG / 2; ++t) {
+                xv[t] = S.x[t];                  // rows >= M duplicate row 0: outputs not stored
+                swap_halves(xv[t]);
             }
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int g = 2 * t + e;
-                uint32_t a0, a1, a2, a3;
-                if constexpr (XLDS) {
-                    const uint2 xw = *reinterpret_cast<const uint2*>(x_rd + (size_t)(gi0 + g) * 128);
-                    unpack_s4x8_x16(xw.x, a0, a1);
-                    unpack_s4x8_x16(xw.y, a2, a3);
-                } else {
-                    unpack_s4x8_x16(e ? xv.z : xv.x, a0, a1);
-                    unpack_s4x8_x16(e ? xv.w : xv.y, a2, a3);
-                }
-                const v4i A = {(int)a0, (int)a1, (int)a2, (int)a3};
-                const uint32_t sxb = sx_l[(gi0 + g) * XR + sx_row];
-#pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    const uint2 w = *reinterpret_cast<const uint2*>(
-                        slab + b * (kStreamSG * 2 * kStreamPlane) + (g * 2 + half) * kStreamPlane + l32 * 8);
-                    uint32_t b0, b1, b2, b3;
-                    unpack_s4x8_x16(w.x, b0, b1);
-                    unpack_s4x8_x16(w.y, b2, b3);
-                    const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
-                    const uint32_t sw2 = (&S.sw[b].x)[g >> 1];
-                    const uint32_t swb = (g & 1) ? (sw2 >> 16) : (sw2 & 0xffffu);
-                    const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (v16i){0}, 0, 0, 0);
-                    const v16f sc = scale_products(sxb, swb);
-#pragma unroll
-                    for (int j = 0; j < NR; ++j)
-                        acc[b][j] = __builtin_fmaf((float)d[j], sc[j], acc[b][j]);
-                }
+        }
+        auto issue = [&](int g, v16i (&d)[NB], v16f (&sc)[NB]) {
+            uint32_t a0, a1, a2, a3;
+            if constexpr (XLDS) {
+                const uint2 xw = *reinterpret_cast<const uint2*>(x_rd + (size_t)(gi0 + g) * 128);
+                unpack_s4x8_x16(xw.x, a0, a1);
+                unpack_s4x8_x16(xw.y, a2, a3);
+            } else {
+                unpack_s4x8_x16((g & 1) ? xv[g >> 1].z : xv[g >> 1].x, a0, a1);
+                unpack_s4x8_x16((g & 1) ? xv[g >> 1].w : xv[g >> 1].y, a2, a3);
             }
+            const v4i A = {(int)a0, (int)a1, (int)a2, (int)a3};
+            const uint32_t sxb = sx_l[(gi0 + g) * XR + sx_row];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const uint2 w = *reinterpret_cast<const uint2*>(
+                    slab + b * (kStreamSG * 2 * kStreamPlane) + (g * 2 + half) * kStreamPlane + l32 * 8);
+                uint32_t b0, b1, b2, b3;
+                unpack_s4x8_x16(w.x, b0, b1);
+                unpack_s4x8_x16(w.y, b2, b3);
+                const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
+                const uint32_t sw2 = (&S.sw[b].x)[g >> 1];
+                const uint32_t swb = (g & 1) ? (sw2 >> 16) : (sw2 & 0xffffu);
+                d[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (v16i){0}, 0, 0, 0);
+                sc[b] = scale_products(sxb, swb);
+            }
+        };
+        v16i d0[NB], d1[NB];
+        v16f s0[NB], s1[NB];
+        issue(0, d0, s0);
+#pragma unroll
+        for (int g = 0; g < kStreamSG; g += 2) {
+            issue(g + 1, d1, s1);
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int j = 0; j < NR; ++j) acc[b][j] = __builtin_fmaf((float)d0[b][j], s0[b][j], acc[b][j]);
+            if (g + 2 < kStreamSG) issue(g + 2, d0, s0);
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+                for (int j = 0; j < NR; ++j) acc[b][j] = __builtin_fmaf((float)d1[b][j], s1[b][j], acc[b][j]);
         }
     };
 
-    StreamStage<NB> buf[PF];
-#pragma unroll
-    for (int d = 0; d < PF; ++d) load(min(d, nst - 1), buf[d]);
     int st = 0;
     for (; st + PF <= nst; st += PF) {
 #pragma unroll
@@ -574,11 +635,14 @@ static size_t stream_smem(int64_t gps, bool xlds) {
            4 * (size_t)kStreamNB * kStreamSG * 2 * kStreamPlane;
 }
 
-static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available, bool allow_split) {
+// scales16: both scale tensors are 16-byte aligned (the streaming kernel reads
+// them 8 groups at a time).
+static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available, bool allow_split,
+                      bool scales16) {
     Plan p;
     p.mr = 32;
     const int64_t G0 = K / 32;
-    if (allow_split && M <= 32 && K % 256 == 0) {
+    if (allow_split && scales16 && M <= 32 && K % 256 == 0) {
         // streaming kernel: one wavefront per 32*kStreamNB weight rows
         p.cfg = 3; p.tm = 32; p.tn = 4 * kStreamNB * 32; p.sg = kStreamSG;
         p.mr = (int)((M + 7) / 8 * 8);
@@ -646,7 +710,8 @@ template <bool PT>
 static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                     uint16_t* y, int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes,
                     float alpha, const float* alpha_dev, hipStream_t stream) {
-    const Plan p = make_plan(M, N, K, workspace ? ws_bytes : 0, !PT);
+    const bool scales16 = ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws)) & 15u) == 0;
+    const Plan p = make_plan(M, N, K, workspace ? ws_bytes : 0, !PT, scales16);
     WUSH_REQUIRE((N + p.tn - 1) / p.tn <= 0x7fffffffLL && (M + p.tm - 1) / p.tm <= 65535);
     float* partial = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int m = (int)M, n = (int)N, k = (int)K;
@@ -689,7 +754,7 @@ extern "C" {
 
 size_t wush_gemm_s4_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 32) return 0;
-    const wush::Plan p = wush::make_plan(M, N, K, (size_t)-1, true);
+    const wush::Plan p = wush::make_plan(M, N, K, (size_t)-1, true, true);
     return p.splits > 1 ? (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
