@@ -280,8 +280,10 @@ def test_gemm_group_dots_exact_per_group(capi):
 @pytest.mark.parametrize("M", [1, 8, 17, 32])
 def test_gemm_scale_alignment_paths_agree(capi, M):
     # Scales that are only 2-byte aligned take the LDS-tiled kernel, 16-byte
-    # aligned ones the streaming kernel (decode M, K % 256 == 0).  Both fold
-    # the same exact group dots in the same group order: equal bit for bit.
+    # aligned ones a streaming kernel (decode M, K % 256 == 0).  For M > 8
+    # both fold the same exact group dots in the same group order: equal bit
+    # for bit.  The M <= 8 streaming kernel sums even and odd groups in two
+    # chains, so there the two agree to fp16 rounding only.
     import torch
     g = rng(4250 + M)
     N, K = 300, 1024
@@ -300,7 +302,10 @@ def test_gemm_scale_alignment_paths_agree(capi, M):
         torch.cuda.synchronize()
         outs.append(f16_tensor_f64(y))
         assert rel_fro(outs[-1], ref) < FRO_TOL, (M, shift, rel_fro(outs[-1], ref))
-    assert np.array_equal(outs[0], outs[1])
+    if M > 8:
+        assert np.array_equal(outs[0], outs[1])
+    else:
+        assert rel_fro(outs[1], outs[0]) < 1e-3
 
 
 def test_gemm_golden_fixture(capi):
