@@ -5,7 +5,6 @@ and the torch module wush_int4_kernel_amd._C in place; `my_int4` then imports
 them.  The compile steps live in wush_int4_kernel_amd/_build.py.
 """
 import os
-import sys
 
 from setuptools import Command, setup
 
@@ -23,9 +22,14 @@ class BuildExtInPlace(Command):
         pass
 
     def run(self):
-        sys.path.insert(0, HERE)
-        from wush_int4_kernel_amd import _build
-        for path in _build.build(verbose=True):
+        # load the build script by path: importing the package would import
+        # its (not yet built) native module
+        import importlib.util
+        spec = importlib.util.spec_from_file_location(
+            "wush_int4_kernel_amd_build", os.path.join(HERE, "wush_int4_kernel_amd", "_build.py"))
+        build = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(build)
+        for path in build.build(verbose=True):
             print("built", path)
 
 

@@ -5,7 +5,8 @@
 //   then the quant_int4 chain on the fp32 x' (no bf16 rounding of x').
 // Transformed activations never touch HBM.
 //
-// Two launch shapes, one numerics:
+// Two launch shapes, one numerics (the small-M per-pair steps live in
+// fused_tq_device.h):
 //  * rows kernel (rows >= 64): lane = row, wavefront = 64 rows of one block c.
 //    T[c] is wave-uniform, so it is read with scalar loads into SGPRs and
 //    every product is v_mul with an SGPR operand: no LDS and no cross-lane
@@ -18,23 +19,10 @@
 //    computes x'_j with T[c][j] read as 64 coalesced bytes and x broadcast
 //    from LDS; the group sums are then re-run in i-order by every lane from
 //    LDS (so they keep the sequential order) and lane pairs pack nibbles.
-#include "wush_device.h"
+#include "fused_tq_device.h"
 #include "../../include/wush_int4.h"
 
 namespace wush {
-
-__device__ __forceinline__ void load_bf16x32(const uint16_t* p, float (&v)[32]) {
-    const uint4* p4 = reinterpret_cast<const uint4*>(p);
-    uint4 r[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) r[c] = p4[c];
-    const uint32_t* u = reinterpret_cast<const uint32_t*>(r);
-#pragma unroll
-    for (int d = 0; d < 16; ++d) {
-        v[2 * d] = bf16_to_f32(u[d] & 0xffffu);
-        v[2 * d + 1] = __uint_as_float(u[d] & 0xffff0000u);
-    }
-}
 
 constexpr int kRowsPerWave = 64;
 constexpr int kBlocksPerWg = 4;
@@ -97,40 +85,14 @@ __global__ __launch_bounds__(64) void fused_tq_smallm_kernel(const uint16_t* __r
     const int64_t C = K >> 5;
     const int64_t p = (int64_t)blockIdx.x * kPairsPerWg + pl;
     const bool active = p < rows * C;
-    const int64_t r = active ? p / C : 0;
-    const int64_t c = active ? p % C : 0;
 
-    xs[pl][j] = active ? bf16_to_f32(x[r * K + c * 32 + j]) : 0.0f;
-    float tj[32];
-    if (active) {
-        load_bf16x32(t + c * 1024 + j * 32, tj);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) tj[i] = 0.0f;
-    }
+    uint4 tj[4];
+    tq_pair_load(x, t, K, p, active, j, xs[pl], tj);
     __syncthreads();
-
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) acc = acc + xs[pl][i] * tj[i];
-    xps[pl][j] = acc;
+    const float xj = tq_pair_matvec(xs[pl], tj);
+    xps[pl][j] = xj;
     __syncthreads();
-
-    float s1 = 0.0f, s2 = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        const float v = xps[pl][i];
-        s1 = s1 + v;
-        s2 = s2 + v * v;
-    }
-    float sf;
-    const uint32_t sb = group_scale(s1, s2, &sf);
-    const int code = code_of(acc, sf) & 0xF;
-    const int partner = __shfl_xor(code, 1, 32);
-    if (active) {
-        if ((j & 1) == 0) q[p * 16 + (j >> 1)] = (uint8_t)(code | (partner << 4));
-        if (j == 0) s[p] = (uint16_t)sb;
-    }
+    tq_pair_quant(xps[pl], xj, j, active, p, q, s);
 }
 
 }  // namespace wush

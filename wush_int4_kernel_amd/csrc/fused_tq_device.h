@@ -1,0 +1,78 @@
+// fused_tq_device.h -- one (row, block) pair of the WUSH transform fused with
+// the INT4 group quantization, handled by 32 lanes (csrc/fused_tq_int4.cu:27-85;
+// tests/test_sw2.py:12-24 fix the arithmetic):
+//   x'_j = sum_{i=0..31} x_i * T[c][j][i]   (fp32, i ascending, mul then add)
+//   then the quant_int4 chain on the fp32 x' (no bf16 rounding of x').
+// Lane j computes x'_j from T[c][j] (64 coalesced bytes) and x broadcast from
+// LDS; the group sums are re-run in i-order by every lane from LDS so they
+// keep the sequential order, and lane pairs pack the nibbles.  These are the
+// steps of the small-M fused_tq kernel.
+#pragma once
+#include "wush_device.h"
+
+namespace wush {
+
+__device__ __forceinline__ void load_bf16x32(const uint16_t* p, float (&v)[32]) {
+    const uint4* p4 = reinterpret_cast<const uint4*>(p);
+    uint4 r[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = p4[c];
+    const uint32_t* u = reinterpret_cast<const uint32_t*>(r);
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+        v[2 * d] = bf16_to_f32(u[d] & 0xffffu);
+        v[2 * d + 1] = __uint_as_float(u[d] & 0xffff0000u);
+    }
+}
+
+// Step 1: lane j stages x_j of pair p = r*C + c in LDS (xs_l, 32 floats) and
+// loads row j of T[c] as raw bf16 pairs (element 2d in the low half of word
+// d).  A barrier must follow before step 2.
+__device__ __forceinline__ void tq_pair_load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ t,
+                                             int64_t K, int64_t p, bool active, int j, float* xs_l,
+                                             uint4 (&tj)[4]) {
+    const int64_t C = K >> 5;
+    const int64_t r = active ? p / C : 0;
+    const int64_t c = active ? p % C : 0;
+    xs_l[j] = active ? bf16_to_f32(x[r * K + c * 32 + j]) : 0.0f;
+    const uint4* row = reinterpret_cast<const uint4*>(t + c * 1024 + j * 32);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) tj[k] = active ? row[k] : make_uint4(0, 0, 0, 0);
+}
+
+// Step 2: x'_j (T converted to fp32 as it is used).  The caller stores it
+// to LDS (xps_l[j]) and syncs.
+__device__ __forceinline__ float tq_pair_matvec(const float* xs_l, const uint4 (&tj)[4]) {
+    const uint32_t* u = &tj[0].x;
+    float acc = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+        acc = acc + xs_l[2 * d] * bf16_to_f32(u[d] & 0xffffu);
+        acc = acc + xs_l[2 * d + 1] * __uint_as_float(u[d] & 0xffff0000u);
+    }
+    return acc;
+}
+
+// Step 3: the group's sums in i-order, its scale, lane j's code; even lanes
+// store one byte (element j low nibble, j+1 high), lane 0 the scale.  The 32
+// lanes of a pair must be one half of a wavefront.
+__device__ __forceinline__ void tq_pair_quant(const float* xps_l, float xj, int j, bool active, int64_t p,
+                                              uint8_t* q, uint16_t* s) {
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const float v = xps_l[i];
+        s1 = s1 + v;
+        s2 = s2 + v * v;
+    }
+    float sf;
+    const uint32_t sb = group_scale(s1, s2, &sf);
+    const int code = code_of(xj, sf) & 0xF;
+    const int partner = __shfl_xor(code, 1, 32);
+    if (active) {
+        if ((j & 1) == 0) q[p * 16 + (j >> 1)] = (uint8_t)(code | (partner << 4));
+        if (j == 0) s[p] = (uint16_t)sb;
+    }
+}
+
+}  // namespace wush
