@@ -6,9 +6,11 @@ bf16, for the Llama-70B FFN shape K=8192, N=57344 at M = 1 / 8 / 32 / 4096.
 
 A "step" is one forward pass of the layer's hot path over one batch of
 synthetic activations, exactly as the reference's official bench chains it
-(reference bench/exp_p13_official.py:31-39):
-  M <= 8 : fused transform+quant -> w4a4_gemv / w4a4_gemv_multi
-  M >  8 : fused transform+quant -> w4a4_gemm_s4
+(reference bench/exp_p13_official.py:31-39; my_int4.chain.make_chain):
+  M == 1 : fused_transform_quant_int4_smallm -> w4a4_gemv
+  M <= 4 : fused_transform_quant_int4_smallm -> w4a4_gemv_multi
+  M <= 32: fused_transform_quant_int4_smallm -> w4a4_gemm_s4
+  else   : fused_transform_quant_int4_v3     -> w4a4_gemm_s4
 with the weights pre-quantized (W' = W T^-1, sigma-clip s4 + bf16 scales) and
 resident in HBM.  One HIP graph holds one chain per distinct weight copy (the copies together
 exceed the 256 MB MALL, so every step streams its weights from HBM), the way a
@@ -98,6 +100,7 @@ def main():
     import torch
     from my_int4 import _C
     from wush_int4_kernel_amd import capi
+    from my_int4.chain import make_chain, route
     from wush_int4_kernel_amd.wush_transform import compute_wush_transform, transform_weights
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -132,11 +135,8 @@ def main():
     stream = torch.cuda.current_stream()
 
     def chain_fn(X, wq_, ws_, M):
-        if M == 1:
-            return lambda: _C.w4a4_gemv(*_C.fused_transform_quant_int4_smallm(X, T), wq_, ws_)
-        if M <= 8:
-            return lambda: _C.w4a4_gemv_multi(*_C.fused_transform_quant_int4_smallm(X, T), wq_, ws_)
-        return lambda: _C.w4a4_gemm_s4(*_C.fused_transform_quant_int4_v3(X, T), wq_, ws_)
+        # the reference's dispatch by M (bench/exp_p13_official.py:31-39)
+        return make_chain(X, T, wq_, ws_, M)
 
     def capture(fns):
         """One HIP graph holding one layer step per function (one per weight
@@ -197,7 +197,7 @@ def main():
         del graph
         entry = {
             "us": round(t_int4 * 1e6, 2),
-            "chain": ("fused_tq(smallm)+gemv" if M <= 8 else "fused_tq+gemm_s4"),
+            "chain": " -> ".join(route(M)),
             "layer_bytes": layer_bytes(M, N, K),
             "hbm_gbs": round(layer_bytes(M, N, K) / t_int4 / 1e9, 1),
             "hbm_frac": round(layer_bytes(M, N, K) / t_int4 / 1e9 / HBM_PEAK_GBS, 4),
@@ -277,7 +277,7 @@ def main():
         "data": "synthetic: seeded N(0,1) activations with 1% outlier channels x50, N(0,0.02) weights "
                 "transformed by this build's WUSH T and sigma-clip quantized",
         "config": {
-            "workload": f"Llama-70B FFN layer K={K} N={N}, M=1: fused_tq(smallm) + gemv_int4, "
+            "workload": f"Llama-70B FFN layer K={K} N={N}, M=1: fused_transform_quant_int4_smallm + w4a4_gemv, "
                         f"one HIP graph of {args.copies} layer steps over distinct weight copies",
             "K": K, "N": N, "M": 1,
         },
