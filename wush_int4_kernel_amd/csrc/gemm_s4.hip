@@ -292,8 +292,8 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
 // transposing writes and the fragment reads bank-conflict-free, and no
 // workgroup barrier is needed.  Activations (<= 32 rows, L2-resident) are
 // loaded as whole 16-byte groups and re-paired across lane halves with
-// v_permlane32_swap; at M <= 8 (XLDS) the slice's activation codes are staged
-// once in LDS instead.  Weight scales arrive as one 16-byte load per row and
+// v_permlane32_swap (M <= 8 has its own kernel, gemm_s4_stream8_kernel,
+// below).  Weight scales arrive as one 16-byte load per row and
 // stage; the bf16 x scales of the slice sit in LDS.  Requires K % 256 == 0
 // and slices of whole stages.
 constexpr int kStreamSG = 8;                     // groups per stage
@@ -317,7 +317,7 @@ struct StreamStage {
     uint4 sw[NB];       // 8 bf16 weight scales of this lane's column
 };
 
-template <int MR, int NB, int PF, bool XLDS>
+template <int MR, int NB, int PF>
 __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __restrict__ xq,
                                                              const uint16_t* __restrict__ xs,
                                                              const uint8_t* __restrict__ wq,
@@ -327,9 +327,8 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
                                                              int M, int N, int K, int groups_per_split) {
     constexpr int NR = MR / 2;
     constexpr int kSlab = NB * kStreamSG * 2 * kStreamPlane;    // bytes of one wavefront's slab
-    constexpr int XR = XLDS ? 8 : 32;            // activation rows staged per group
+    constexpr int XR = 32;                       // activation rows staged per group
     static_assert(MR % 8 == 0 && MR <= 32, "fold rows");
-    static_assert(!XLDS || MR == 8, "LDS-resident activations only for M <= 8");
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -341,8 +340,7 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
     const int g_end = min(G, g_begin + groups_per_split);
     const int gcount = g_end - g_begin;          // multiple of kStreamSG
     uint16_t* sx_l = reinterpret_cast<uint16_t*>(smem);                    // bf16 [gcount][XR]
-    uint8_t* x_l = smem + (size_t)groups_per_split * XR * sizeof(uint16_t); // XLDS: [gcount][2][8][8 B]
-    uint8_t* slab = x_l + (XLDS ? (size_t)groups_per_split * 128 : 0) + (size_t)wave * kSlab;
+    uint8_t* slab = smem + (size_t)groups_per_split * XR * sizeof(uint16_t) + (size_t)wave * kSlab;
 
     // Wavefronts past the last row block (only in the last workgroup) stream
     // clamped rows and store nothing.
@@ -369,10 +367,6 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
         sp[b] = ws + (size_t)(n < N ? n : N - 1) * G + g_begin;
     }
     const uint8_t* xp = xq + (size_t)(l32 < M ? l32 : 0) * K2 + (size_t)(g_begin + half) * 16;
-    // LDS-resident activations (MR == 8): MFMA rows 8..31 repeat rows 0..7;
-    // only accumulator rows 0..7 are folded, so their content is irrelevant
-    const uint8_t* x_rd = x_l + half * 64 + (l32 & 7) * 8;
-    const int sx_row = XLDS ? (l32 & 7) : l32;
 
     float acc[NB][NR];
 #pragma unroll
@@ -394,10 +388,8 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
             }
             S.sw[b] = *reinterpret_cast<const uint4*>(sp[b] + st * kStreamSG);
         }
-        if constexpr (!XLDS) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) S.x[t] = *reinterpret_cast<const uint4*>(xp + off + (size_t)t * 32);
-        }
+        for (int t = 0; t < 4; ++t) S.x[t] = *reinterpret_cast<const uint4*>(xp + off + (size_t)t * 32);
     };
 
     // The first stages' weights do not depend on the staged data: request
@@ -406,7 +398,7 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
 #pragma unroll
     for (int d = 0; d < PF; ++d) load(min(d, nst - 1), buf[d]);
 
-    // Stage the slice's x scales (and at M <= 8 its activation codes) in LDS.
+    // Stage the slice's x scales in LDS.
     // All of a thread's loads are issued before its LDS stores, so the
     // staging costs one L2 round trip, not one per element.
     {
@@ -438,31 +430,6 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
             }
         }
     }
-    if constexpr (XLDS) {
-        // activation codes of the slice, fragment-major [group][k-half][row][8 B]
-        constexpr int U = 8;
-        const int nchunk = gcount * 8;
-        for (int c0 = threadIdx.x; c0 < nchunk; c0 += 256 * U) {
-            uint4 v[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int c = c0 + u * 256;
-                const int g = c >> 3, m = c & 7;
-                v[u] = (c < nchunk && m < M)
-                           ? *reinterpret_cast<const uint4*>(xq + (size_t)m * K2 + (size_t)(g_begin + g) * 16)
-                           : make_uint4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int c = c0 + u * 256;
-                if (c < nchunk) {
-                    const int g = c >> 3, m = c & 7;
-                    *reinterpret_cast<uint2*>(x_l + (size_t)g * 128 + m * 8) = make_uint2(v[u].x, v[u].y);
-                    *reinterpret_cast<uint2*>(x_l + (size_t)g * 128 + 64 + m * 8) = make_uint2(v[u].z, v[u].w);
-                }
-            }
-        }
-    }
     __syncthreads();
     if (nb0 * 32 >= N) return;
 
@@ -485,25 +452,17 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
         //    group g, so the fold overlaps the MFMA latency of the next group.
         const int gi0 = st * kStreamSG;
         uint4 xv[kStreamSG / 2];
-        if constexpr (!XLDS) {
 #pragma unroll
-            for (int t = 0; t < kStreamSG / 2; ++t) {
-                xv[t] = S.x[t];                  // rows >= M duplicate row 0: outputs not stored
-                swap_halves(xv[t]);
-            }
+        for (int t = 0; t < kStreamSG / 2; ++t) {
+            xv[t] = S.x[t];                      // rows >= M duplicate row 0: outputs not stored
+            swap_halves(xv[t]);
         }
         auto issue = [&](int g, v16i (&d)[NB], v16f (&sc)[NB]) {
             uint32_t a0, a1, a2, a3;
-            if constexpr (XLDS) {
-                const uint2 xw = *reinterpret_cast<const uint2*>(x_rd + (size_t)(gi0 + g) * 128);
-                unpack_s4x8_x16(xw.x, a0, a1);
-                unpack_s4x8_x16(xw.y, a2, a3);
-            } else {
-                unpack_s4x8_x16((g & 1) ? xv[g >> 1].z : xv[g >> 1].x, a0, a1);
-                unpack_s4x8_x16((g & 1) ? xv[g >> 1].w : xv[g >> 1].y, a2, a3);
-            }
+            unpack_s4x8_x16((g & 1) ? xv[g >> 1].z : xv[g >> 1].x, a0, a1);
+            unpack_s4x8_x16((g & 1) ? xv[g >> 1].w : xv[g >> 1].y, a2, a3);
             const v4i A = {(int)a0, (int)a1, (int)a2, (int)a3};
-            const uint32_t sxb = sx_l[(gi0 + g) * XR + sx_row];
+            const uint32_t sxb = sx_l[(gi0 + g) * XR + l32];
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 const uint2 w = *reinterpret_cast<const uint2*>(
@@ -850,19 +809,15 @@ constexpr int kStreamPF = WUSH_STREAM_PF;        // stages of loads in flight pe
 #ifndef WUSH_STREAM_PFX
 #define WUSH_STREAM_PFX 2
 #endif
-constexpr int kStreamPFX = WUSH_STREAM_PFX;      // same, M <= 8 (activations in LDS)
+constexpr int kStreamPFX = WUSH_STREAM_PFX;      // same, M <= 8 kernel
 constexpr size_t kStreamLdsMax = 64 * 1024;
 
-#ifndef WUSH_STREAM8
-#define WUSH_STREAM8 1           // M <= 8: 16x16x64 block-diagonal kernel
-#endif
-
-static size_t stream_smem(int64_t gps, bool xlds) {
-    if (xlds && WUSH_STREAM8)
-        return (size_t)gps * (16 + 128) + kStream8ZeroBytes + 4 * (size_t)kStreamSG * 2 * kStreamPlane;
-    const size_t xr = xlds ? 8 : 32;
-    return (size_t)gps * xr * sizeof(uint16_t) + (xlds ? (size_t)gps * 128 : 0) +
-           4 * (size_t)kStreamNB * kStreamSG * 2 * kStreamPlane;
+// LDS bytes of a streaming launch with gps groups per slice: M <= 8 stages
+// x scales (4 B per group pair and row) and codes (128 B per group) plus the
+// zero words; M > 8 stages bf16 x scales of 32 rows.  Plus the four slabs.
+static size_t stream_smem(int64_t gps, bool m8) {
+    if (m8) return (size_t)gps * (16 + 128) + kStream8ZeroBytes + 4 * (size_t)kStreamSG * 2 * kStreamPlane;
+    return (size_t)gps * 32 * sizeof(uint16_t) + 4 * (size_t)kStreamNB * kStreamSG * 2 * kStreamPlane;
 }
 
 // scales16: both scale tensors are 16-byte aligned (the streaming kernel reads
@@ -877,20 +832,20 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         p.cfg = 3; p.tm = 32; p.tn = 4 * kStreamNB * 32; p.sg = kStreamSG;
         p.mr = (int)((M + 7) / 8 * 8);
         const int64_t waves = (N + 32 * kStreamNB - 1) / (32 * kStreamNB);
-        static_assert(!WUSH_STREAM8 || kStreamNB == 1, "the M <= 8 kernel streams one 32-row block per wavefront");
+        static_assert(kStreamNB == 1, "the M <= 8 kernel streams one 32-row block per wavefront");
         int s = 1;
         while (s < 16 && waves * s < WUSH_STREAM_WAVES && G0 / (2 * s) >= 4 * kStreamSG) s *= 2;
         int64_t gps = (G0 + s - 1) / s;
         gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
-        const bool xlds = p.mr == 8;
-        while (stream_smem(gps, xlds) > kStreamLdsMax && gps > kStreamSG) {
+        const bool m8 = p.mr == 8;
+        while (stream_smem(gps, m8) > kStreamLdsMax && gps > kStreamSG) {
             s *= 2;
             gps = (G0 + s - 1) / s;
             gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
         }
         s = (int)((G0 + gps - 1) / gps);
         const bool ws_ok = s == 1 || (size_t)s * (size_t)M * (size_t)N * sizeof(float) <= ws_bytes_available;
-        if (ws_ok && stream_smem(gps, xlds) <= kStreamLdsMax) {
+        if (ws_ok && stream_smem(gps, m8) <= kStreamLdsMax) {
             p.splits = s;
             p.groups_per_split = (int)gps;
             return p;
@@ -951,15 +906,10 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
             const size_t smem = stream_smem(p.groups_per_split, p.mr == 8);
             dim3 grid((unsigned)((N + p.tn - 1) / p.tn), (unsigned)p.splits);
             switch (p.mr) {
-                case 8:
-                    if (WUSH_STREAM8)
-                        gemm_s4_stream8_kernel<kStreamPFX><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
-                    else
-                        gemm_s4_stream_kernel<8, kStreamNB, kStreamPFX, true><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
-                    break;
-                case 16: gemm_s4_stream_kernel<16, kStreamNB, kStreamPF, false><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
-                case 24: gemm_s4_stream_kernel<24, kStreamNB, kStreamPF, false><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
-                default: gemm_s4_stream_kernel<32, kStreamNB, kStreamPF, false><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                case 8: gemm_s4_stream8_kernel<kStreamPFX><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                case 16: gemm_s4_stream_kernel<16, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                case 24: gemm_s4_stream_kernel<24, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                default: gemm_s4_stream_kernel<32, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
             }
         }
     } else if (p.cfg == 0) {
