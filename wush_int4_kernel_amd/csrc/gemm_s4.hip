@@ -822,6 +822,12 @@ static size_t stream_smem(int64_t gps, bool m8) {
 
 // scales16: both scale tensors are 16-byte aligned (the streaming kernel reads
 // them 8 groups at a time).
+#ifndef WUSH_PF_BM
+#define WUSH_PF_BM 2             // prefill tile: 32x32 blocks per wavefront along M
+#endif
+#ifndef WUSH_PF_BN
+#define WUSH_PF_BN 2             // and along N (2 x 2 wavefronts per workgroup)
+#endif
 static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available, bool allow_split,
                       bool scales16) {
     Plan p;
@@ -858,7 +864,7 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
     } else if (M <= 64) {
         p.cfg = 1; p.tm = 64; p.tn = 128; p.sg = 8;
     } else {
-        p.cfg = 2; p.tm = 128; p.tn = 128; p.sg = 4;
+        p.cfg = 2; p.tm = 32 * WUSH_PF_BM * 2; p.tn = 32 * WUSH_PF_BN * 2; p.sg = 4;
     }
     const int64_t G = K / 32;
     const int64_t tiles = ((M + p.tm - 1) / p.tm) * ((N + p.tn - 1) / p.tn);
@@ -924,7 +930,7 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     } else if (p.cfg == 1) {
         launch_gemm<1, 2, 2, 2, 8, 32, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
     } else {
-        launch_gemm<2, 2, 2, 2, 4, 32, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
+        launch_gemm<WUSH_PF_BM, WUSH_PF_BN, 2, 2, 4, 32, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
     }
     if (p.splits > 1) {
         const int64_t MN = M * N;
