@@ -44,6 +44,7 @@ METRIC = "µs/layer + speedup vs hipBLASLt bf16, K=8192 N=57344 at M=1/8/32/4096
 K_L70, N_L70 = 8192, 57344
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
+VALU_PEAK_LANE_OPS = 256 * 4 * 16 * 2.4e9   # 256 CUs x 4 SIMDs x 16 lanes per cycle x 2.4 GHz (no packed fp32)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_int4_l70_m1_traffic.txt")
 
 
@@ -217,6 +218,45 @@ def main():
         layers[f"M={M}"] = entry
         log(f"[bench] M={M}: {entry}")
 
+    # ---------------------------------------- the path's other ops, timed alone
+    ops = {}
+    # fused transform + quant of X 2048x4096 (1% outlier channels x50),
+    # T from this build's WUSH solve on a 512-row calibration draw; VALU-bound when bit-exact
+    Mc, Kc = 2048, 4096
+    gc = torch.Generator(device=dev).manual_seed(1)
+    och = torch.randperm(Kc, generator=gcpu)[:int(round(0.01 * Kc))].to(dev)
+
+    def acts_c(m):
+        x = torch.randn(m, Kc, generator=gc, device=dev, dtype=torch.float32)
+        x[:, och] *= 50.0
+        return x
+
+    Xc2 = acts_c(Mc).to(torch.bfloat16)
+    Wc2 = torch.randn(Kc, Kc, generator=gc, device=dev, dtype=torch.float32) * 0.02
+    Tc2 = compute_wush_transform(acts_c(512).double(), Wc2.double()).to(torch.bfloat16).contiguous()
+    reps = 10
+    g2 = capture([lambda: _C.fused_transform_quant_int4(Xc2, Tc2)] * reps)
+    t = time_graph(g2, reps, args.steps, args.warmup)
+    del g2
+    tq_bytes = 2 * Mc * Kc + 64 * Kc + Mc * Kc // 2 + Mc * Kc // 16
+    tq_lane_ops = 64 * Mc * Kc          # one mul and one add per MAC, 32 MACs per element
+    ops["fused_tq_cfg2"] = {
+        "us": round(t * 1e6, 2), "shape": f"X {Mc}x{Kc} bf16, T {Kc // 32}x32x32",
+        "hbm_bytes": tq_bytes, "hbm_gbs": round(tq_bytes / t / 1e9, 1),
+        "hbm_frac": round(tq_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
+        "valu_lane_ops": tq_lane_ops, "valu_frac": round(tq_lane_ops / t / VALU_PEAK_LANE_OPS, 4),
+    }
+    # a2/a3: quant_int4 of one Llama-70B weight tensor (N x K bf16), HBM-bound
+    g3 = capture([lambda: _C.quant_int4(Wt)] * 2)
+    t = time_graph(g3, 2, max(4, args.steps // 20), 2)
+    del g3
+    q_bytes = N * K * 2 + N * K // 2 + N * K // 16
+    ops["quant_int4_l70_weights"] = {
+        "us": round(t * 1e6, 2), "shape": f"{N}x{K} bf16", "hbm_bytes": q_bytes,
+        "hbm_gbs": round(q_bytes / t / 1e9, 1), "hbm_frac": round(q_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
+    }
+    log(f"[bench] ops: {ops}")
+
     # --------------------------------------------- roofline of the M=1 kernel
     M = 1
     X = activations(M, gdev).to(torch.bfloat16)
@@ -282,6 +322,7 @@ def main():
             "K": K, "N": N, "M": 1,
         },
         "layers": layers,
+        "ops": ops,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "device": torch.cuda.get_device_name(0),

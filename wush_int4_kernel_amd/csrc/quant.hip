@@ -62,6 +62,48 @@ struct InputTraits<WUSH_DTYPE_F32> {
     }
 };
 
+// Codes of bf16 or fp16 inputs without a division per element.
+// Write sf = ms * 2^es (ms < 256, sf is a normal bf16) and v = mv * 2^ev
+// (|mv| < 2^11).  For a half-integer h, v/sf - h = (2v - 2h*sf) / (2 sf) and
+// the numerator is a multiple of 2^min(ev+1, es); if it is not zero and
+// |v/sf| is near h >= 0.5 (so 2^(ev-es) >= 0.5*128/2047), then
+// |v/sf - h| >= 2^(ev-es)/255 > 2^-13.  With r = RN(1/sf) and y = RN(v*r),
+// |y - v/sf| < 2^-20 for |v/sf| < 8.  Hence rint(y) == rint(RN(v/sf)) except
+// when v/sf is exactly a half-integer, and then |y - h| < 2^-20: such y
+// (within kHalfBand of a half-integer) are replaced by floor(y) + 0.5 = h
+// and rounded half to even like the reference.  |y| >= 8 clamps like
+// |v/sf| > 7.5; NaN and infinities give the codes of code_of.  Bit-identical
+// to code_of for bf16 and fp16 inputs; fp32 inputs keep the division.
+constexpr float kHalfBand = 0x1p-14f;
+__device__ __forceinline__ int code_of_narrow(float v, float r) {
+    const float y = v * r;
+    const float f = __builtin_floorf(y);
+    const float y2 = __builtin_fabsf(y - f - 0.5f) < kHalfBand ? f + 0.5f : y;
+    float c = __builtin_rintf(y2);
+    c = __builtin_fminf(__builtin_fmaxf(c, -7.0f), 7.0f);
+    return (y == y) ? (int)c : 0;
+}
+
+__device__ __forceinline__ uint32_t quant_group32_narrow(const float (&v)[32], uint32_t (&w)[4]) {
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        s1 = s1 + v[i];
+        s2 = s2 + v[i] * v[i];
+    }
+    float sf;
+    const uint32_t sb = group_scale(s1, s2, &sf);
+    const float r = 1.0f / sf;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint32_t acc = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc |= (uint32_t)(code_of_narrow(v[d * 8 + e], r) & 0xF) << (4 * e);
+        w[d] = acc;
+    }
+    return sb;
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void quant_int4_kernel(const void* __restrict__ x,
                                                          uint8_t* __restrict__ q,
@@ -72,7 +114,7 @@ __global__ __launch_bounds__(256) void quant_int4_kernel(const void* __restrict_
     float v[32];
     InputTraits<DT>::load(x, g, v);
     uint32_t w[4];
-    uint32_t sb = quant_group32(v, w);
+    const uint32_t sb = DT == WUSH_DTYPE_F32 ? quant_group32(v, w) : quant_group32_narrow(v, w);
     reinterpret_cast<uint4*>(q)[g] = make_uint4(w[0], w[1], w[2], w[3]);
     s[g] = (uint16_t)sb;
 }
