@@ -277,6 +277,18 @@ def test_gemm_group_dots_exact_per_group(capi):
             assert np.array_equal(y, D[: y.shape[0], :, gg].astype(np.float64)), (kernel, gg)
 
 
+@pytest.mark.parametrize("M", [1, 5, 8])
+def test_gemm_decode_many_row_blocks(capi, M):
+    # N/32 >= 1024 row blocks: the 32-row streaming kernel with workgroup-staged
+    # activations (fewer blocks take the 16-row kernel); N not a multiple of 32
+    g = rng(4270 + M)
+    N, K = 33000, 512
+    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    y = run_gemm(capi, xq, xs, wq, ws)
+    ref = oracle.gemm_f64(xq, xs, wq, ws)
+    assert rel_fro(y, ref) < FRO_TOL, (M, rel_fro(y, ref))
+
+
 @pytest.mark.parametrize("M", [1, 8, 17, 32])
 def test_gemm_scale_alignment_paths_agree(capi, M):
     # Scales that are only 2-byte aligned take the LDS-tiled kernel, 16-byte

@@ -748,6 +748,175 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
     }
 }
 
+// ----------------------------------- streaming kernel, M <= 8, 16-row waves
+// The MFMA scheme of gemm_s4_stream8_kernel (16x16x64 int8 over a group pair
+// with a block-diagonal activation operand, fold factors from a 16x16x16
+// bf16 MFMA), but each wavefront owns 16 weight rows -- twice the
+// wavefronts for the same N, which is what keeps HBM busy: a load-only probe
+// of this stream reads 6.1 TB/s with 16-row wavefronts against 5.4 TB/s with
+// 32-row ones -- and nothing is staged per workgroup: every stage of 8 groups
+// brings, per wavefront, 16 rows x 128 B of weights (2 load instructions),
+// the 8 activation rows' codes of those groups (1 instruction, L2-resident)
+// and both scale slices in registers, and goes through a wavefront-private
+// LDS slab (weights [group][half][row][8 B], activations [group][half][m][8 B]).
+// Off-diagonal activation lanes read a shared block of zero words.  No
+// workgroup barrier is needed after the zero fill.
+constexpr int kS16WPlane = 16 * 8 + 16;          // weight slab plane: 16 rows x 8 B + pad
+constexpr int kS16XPlane = 8 * 8 + 8;            // activation slab plane: 8 rows x 8 B + pad
+constexpr int kS16Slab = kStreamSG * 2 * (kS16WPlane + kS16XPlane);
+constexpr int kS16Zero = 1024;                   // zero words (pairs 0..3 at 4 * kS16XPlane each)
+constexpr int kS16Waves = 4;
+
+template <int PF>
+__global__ __launch_bounds__(256) void gemm_s4_stream16_kernel(const uint8_t* __restrict__ xq,
+                                                               const uint16_t* __restrict__ xs,
+                                                               const uint8_t* __restrict__ wq,
+                                                               const uint16_t* __restrict__ ws,
+                                                               uint16_t* __restrict__ y,
+                                                               float* __restrict__ partial,
+                                                               int M, int N, int K, int groups_per_split) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    __shared__ __align__(16) uint8_t lds[kS16Zero + kS16Waves * kS16Slab];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int q = lane >> 4;                     // MFMA lane block: k 16q..16q+15 of the pair
+    const int r16 = lane & 15;                   // MFMA row (A: m + 8e) / column (B: n)
+    const int G = K >> 5;
+    const int K2 = K >> 1;
+    const int g_begin = blockIdx.y * groups_per_split;
+    const int g_end = min(G, g_begin + groups_per_split);
+    const int nst = (g_end - g_begin) / kStreamSG;
+    uint8_t* zero = lds;
+    uint8_t* wslab = lds + kS16Zero + wave * kS16Slab;
+    uint8_t* xslab = wslab + kStreamSG * 2 * kS16WPlane;
+
+    if (threadIdx.x < kS16Zero / 16) reinterpret_cast<uint4*>(zero)[threadIdx.x] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+
+    const int n0 = (blockIdx.x * kS16Waves + wave) * 16;
+    if (n0 >= N) return;
+    // weight loads: lane -> row n0 + 8j + lane/8, 16-byte chunk lane%8 of the stage
+    const int wrow = lane >> 3, wg = lane & 7;
+    const uint8_t* wp[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + 8 * j + wrow;
+        wp[j] = wq + (size_t)(n < N ? n : N - 1) * K2 + (size_t)(g_begin + wg) * 16;
+    }
+    // activation loads: lane -> row m = lane/8 (rows >= M repeat row M-1: not stored), group lane%8
+    const int xm = lane >> 3;
+    const uint8_t* xp = xq + (size_t)(xm < M ? xm : M - 1) * K2 + (size_t)(g_begin + wg) * 16;
+    // scale loads: 8 groups of weight row n0 + r16 and of activation row r16 % 8
+    const int sn = n0 + r16;
+    const uint16_t* swp = ws + (size_t)(sn < N ? sn : N - 1) * G + g_begin;
+    const int sm = r16 & 7;
+    const uint16_t* sxp = xs + (size_t)(sm < M ? sm : M - 1) * G + g_begin;
+
+    struct Stage {
+        uint4 w[2];
+        uint4 x;
+        uint4 sw;        // bf16 pairs (2p, 2p+1) of column r16
+        uint4 sx;        // bf16 pairs (2p, 2p+1) of activation row r16 % 8
+    };
+    auto load = [&](int st, Stage& S) {
+        const size_t off = (size_t)st * (kStreamSG * 16);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) S.w[j] = load_nt16(wp[j] + off);
+        S.x = *reinterpret_cast<const uint4*>(xp + off);
+        S.sw = *reinterpret_cast<const uint4*>(swp + st * kStreamSG);
+        S.sx = *reinterpret_cast<const uint4*>(sxp + st * kStreamSG);
+    };
+
+    // MFMA operand addresses.  A: lane (m + 8e, q) holds half q%2 of group
+    // 2p+e of activation row m when q/2 == e, else zeros.
+    const int am = r16 & 7, ae = r16 >> 3;
+    const bool a_data = (q >> 1) == ae;
+    const uint8_t* a_rd = a_data ? xslab + (2 * ae + (q & 1)) * kS16XPlane + am * 8 : zero;
+    const uint32_t sx_mask = ae ? 0xffff0000u : 0x0000ffffu;
+    // B: lane (n, q) holds half q%2 of group 2p + q/2 of weight row n.
+    const uint8_t* b_rd = wslab + q * kS16WPlane + r16 * 8;
+
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto process = [&](Stage& S) {
+        // transpose the stage into the slabs
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            uint8_t* b = wslab + (8 * j + wrow) * 8;
+            *reinterpret_cast<uint2*>(b + (wg * 2 + 0) * kS16WPlane) = make_uint2(S.w[j].x, S.w[j].y);
+            *reinterpret_cast<uint2*>(b + (wg * 2 + 1) * kS16WPlane) = make_uint2(S.w[j].z, S.w[j].w);
+        }
+        {
+            uint8_t* b = xslab + xm * 8;
+            *reinterpret_cast<uint2*>(b + (wg * 2 + 0) * kS16XPlane) = make_uint2(S.x.x, S.x.y);
+            *reinterpret_cast<uint2*>(b + (wg * 2 + 1) * kS16XPlane) = make_uint2(S.x.z, S.x.w);
+        }
+        auto issue = [&](int p, v4i& d, v4f& sc) {
+            const uint2 xw = *reinterpret_cast<const uint2*>(a_rd + p * 4 * kS16XPlane);
+            uint32_t a0, a1, a2, a3;
+            unpack_s4x8_x16(xw.x, a0, a1);
+            unpack_s4x8_x16(xw.y, a2, a3);
+            const v4i A = {(int)a0, (int)a1, (int)a2, (int)a3};
+            const uint2 ww = *reinterpret_cast<const uint2*>(b_rd + p * 4 * kS16WPlane);
+            uint32_t b0, b1, b2, b3;
+            unpack_s4x8_x16(ww.x, b0, b1);
+            unpack_s4x8_x16(ww.y, b2, b3);
+            const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
+            const uint32_t sxa = (&S.sx.x)[p] & sx_mask;
+            const uint2 sa2 = (p & 1) ? make_uint2(0u, sxa) : make_uint2(sxa, 0u);
+            const uint2 sb2 = (p < 2) ? make_uint2(S.sw.x, S.sw.y) : make_uint2(S.sw.z, S.sw.w);
+            d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i){0, 0, 0, 0}, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s, sa2), __builtin_bit_cast(v4s, sb2),
+                                                           (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        };
+        auto fold = [&](const v4i& d, const v4f& sc) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf((float)d[j], sc[j], acc[j]);
+        };
+        v4i d0, d1;
+        v4f s0, s1;
+        issue(0, d0, s0);
+        issue(1, d1, s1);
+        fold(d0, s0);
+        issue(2, d0, s0);
+        fold(d1, s1);
+        issue(3, d1, s1);
+        fold(d0, s0);
+        fold(d1, s1);
+    };
+
+    Stage buf[PF];
+#pragma unroll
+    for (int d = 0; d < PF; ++d) load(min(d, nst - 1), buf[d]);
+    int st = 0;
+    for (; st + PF <= nst; st += PF) {
+#pragma unroll
+        for (int d = 0; d < PF; ++d) {
+            process(buf[d]);
+            load(min(st + d + PF, nst - 1), buf[d]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < PF - 1; ++d)
+        if (st + d < nst) process(buf[d]);
+
+    // even-group sums (lanes 0-31) + odd-group sums (lanes 32-63); lanes 0-31
+    // then hold rows m = 4q + j of column n0 + r16
+    const int col = n0 + r16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float v = (acc[j] + __shfl_xor(acc[j], 32)) * kFold8OutScale;
+        const int row = 4 * q + j;
+        if (lane < 32 && row < M && col < N) {
+            if (partial != nullptr)
+                partial[((size_t)blockIdx.y * M + row) * N + col] = v;
+            else
+                y[(size_t)row * N + col] = f32_to_f16_bits(v);
+        }
+    }
+}
+
 // Sum the split-K partials in slice order and convert to fp16.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial,
                                                             uint16_t* __restrict__ y, int64_t MN,
@@ -815,7 +984,19 @@ constexpr size_t kStreamLdsMax = 64 * 1024;
 // LDS bytes of a streaming launch with gps groups per slice: M <= 8 stages
 // x scales (4 B per group pair and row) and codes (128 B per group) plus the
 // zero words; M > 8 stages bf16 x scales of 32 rows.  Plus the four slabs.
-static size_t stream_smem(int64_t gps, bool m8) {
+// M <= 8 with few 32-row blocks (N/32 below the wavefront target) streams
+// 16 rows per wavefront (gemm_s4_stream16_kernel) instead of splitting K; with
+// many blocks the 32-row kernel, whose activations are staged once per
+// workgroup, is faster (measured: Q8 M=1 14.4 vs 18.7 us, L70 M=8 63.7 vs
+// 58.1 us).
+#ifndef WUSH_STREAM16
+#define WUSH_STREAM16 1
+#endif
+static bool use_stream16(int64_t M, int64_t N) {
+    return WUSH_STREAM16 && M <= 8 && (N + 31) / 32 < WUSH_STREAM_WAVES;
+}
+static size_t stream_smem(int64_t gps, bool m8, bool s16) {
+    if (s16) return 0;                       // static LDS only
     if (m8) return (size_t)gps * (16 + 128) + kStream8ZeroBytes + 4 * (size_t)kStreamSG * 2 * kStreamPlane;
     return (size_t)gps * 32 * sizeof(uint16_t) + 4 * (size_t)kStreamNB * kStreamSG * 2 * kStreamPlane;
 }
@@ -837,21 +1018,24 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         // streaming kernel: one wavefront per 32*kStreamNB weight rows
         p.cfg = 3; p.tm = 32; p.tn = 4 * kStreamNB * 32; p.sg = kStreamSG;
         p.mr = (int)((M + 7) / 8 * 8);
-        const int64_t waves = (N + 32 * kStreamNB - 1) / (32 * kStreamNB);
+        const bool s16 = use_stream16(M, N);
+        const int rows_per_wave = s16 ? 16 : 32 * kStreamNB;
+        p.tn = 4 * rows_per_wave;
+        const int64_t waves = (N + rows_per_wave - 1) / rows_per_wave;
         static_assert(kStreamNB == 1, "the M <= 8 kernel streams one 32-row block per wavefront");
         int s = 1;
         while (s < 16 && waves * s < WUSH_STREAM_WAVES && G0 / (2 * s) >= 4 * kStreamSG) s *= 2;
         int64_t gps = (G0 + s - 1) / s;
         gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
         const bool m8 = p.mr == 8;
-        while (stream_smem(gps, m8) > kStreamLdsMax && gps > kStreamSG) {
+        while (stream_smem(gps, m8, s16) > kStreamLdsMax && gps > kStreamSG) {
             s *= 2;
             gps = (G0 + s - 1) / s;
             gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
         }
         s = (int)((G0 + gps - 1) / gps);
         const bool ws_ok = s == 1 || (size_t)s * (size_t)M * (size_t)N * sizeof(float) <= ws_bytes_available;
-        if (ws_ok && stream_smem(gps, m8) <= kStreamLdsMax) {
+        if (ws_ok && stream_smem(gps, m8, s16) <= kStreamLdsMax) {
             p.splits = s;
             p.groups_per_split = (int)gps;
             return p;
@@ -909,10 +1093,16 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     const int m = (int)M, n = (int)N, k = (int)K;
     if (p.cfg == 3) {
         if constexpr (!PT) {
-            const size_t smem = stream_smem(p.groups_per_split, p.mr == 8);
+            const bool s16 = p.tn == 64;
+            const size_t smem = stream_smem(p.groups_per_split, p.mr == 8, s16);
             dim3 grid((unsigned)((N + p.tn - 1) / p.tn), (unsigned)p.splits);
             switch (p.mr) {
-                case 8: gemm_s4_stream8_kernel<kStreamPFX><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                case 8:
+                    if (s16)
+                        gemm_s4_stream16_kernel<kStreamPFX><<<grid, 256, 0, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
+                    else
+                        gemm_s4_stream8_kernel<kStreamPFX><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
+                    break;
                 case 16: gemm_s4_stream_kernel<16, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
                 case 24: gemm_s4_stream_kernel<24, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
                 default: gemm_s4_stream_kernel<32, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
