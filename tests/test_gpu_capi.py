@@ -161,8 +161,10 @@ def test_fused_golden_fixture(capi):
     assert np.array_equal(q, fz["q"]) and np.array_equal(s, fz["s"])
 
 
+# the small-M kernel serves rows < 384, the rows kernel the rest
 @pytest.mark.parametrize("rows,K", [(1, 32), (1, 4096), (3, 96), (8, 8192), (63, 256), (64, 256),
-                                    (65, 512), (130, 128), (256, 4096), (1 << 16, 64)])
+                                    (65, 512), (130, 128), (256, 4096), (383, 256), (384, 256),
+                                    (385, 96), (1 << 16, 64)])
 def test_fused_random(capi, rows, K):
     g = rng(2000 + rows + K)
     xb = outlier_activations(g, rows, K)

@@ -7,13 +7,13 @@
 //
 // Two launch shapes, one numerics (the small-M per-pair steps live in
 // fused_tq_device.h):
-//  * rows kernel (rows >= 64): lane = row, wavefront = 64 rows of one block c.
+//  * rows kernel (rows >= 384): lane = row, wavefront = 64 rows of one block c.
 //    T[c] is wave-uniform, so it is read with scalar loads into SGPRs and
 //    every product is v_mul with an SGPR operand: no LDS and no cross-lane
 //    traffic in the 2048-op inner loop.  4 wavefronts of a workgroup take 4
 //    adjacent blocks of the same 64 rows, so each row's 256 B of bf16 input
 //    is consumed by one workgroup.
-//  * small-M kernel (rows < 64, decode): 32 lanes per (row, block), two
+//  * small-M kernel (rows < 384: decode, small batches): 32 lanes per (row, block), two
 //    pairs per one-wavefront workgroup so a decode row spreads over K/64 CUs;
 //    lane j
 //    computes x'_j with T[c][j] read as 64 coalesced bytes and x broadcast
@@ -97,6 +97,14 @@ __global__ __launch_bounds__(64) void fused_tq_smallm_kernel(const uint16_t* __r
 
 }  // namespace wush
 
+// Rows below this use the small-M kernel (32 lanes per (row, block)); above
+// it the rows kernel, whose 64-row wavefronts are latency-bound when few
+// (K=8192, T cold: 64 rows 9.1 vs 23.6 us, 256 rows 19.9 vs 24.0 us, 512 rows
+// 32.4 vs 25.3 us).
+#ifndef WUSH_TQ_SMALLM_ROWS
+#define WUSH_TQ_SMALLM_ROWS 384
+#endif
+
 extern "C" int wush_fused_tq(const uint16_t* x, const uint16_t* t, uint8_t* q, uint16_t* s,
                              int64_t rows, int64_t K, hipStream_t stream) {
     WUSH_REQUIRE(rows >= 0 && K > 0 && K % 32 == 0);
@@ -105,7 +113,7 @@ extern "C" int wush_fused_tq(const uint16_t* x, const uint16_t* t, uint8_t* q, u
     WUSH_REQUIRE(((uintptr_t)x & 15u) == 0 && ((uintptr_t)t & 15u) == 0 &&
                  ((uintptr_t)q & 15u) == 0 && ((uintptr_t)s & 1u) == 0);
     const int64_t C = K / 32;
-    if (rows < wush::kRowsPerWave) {
+    if (rows < WUSH_TQ_SMALLM_ROWS) {
         const int64_t blocks = (rows * C + wush::kPairsPerWg - 1) / wush::kPairsPerWg;
         WUSH_REQUIRE(blocks <= 0x7fffffffLL);
         wush::fused_tq_smallm_kernel<<<(unsigned)blocks, 64, 0, stream>>>(x, t, q, s, rows, K);
