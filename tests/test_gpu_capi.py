@@ -281,8 +281,8 @@ def test_gemm_group_dots_exact_per_group(capi):
 
 @pytest.mark.parametrize("M", [1, 5, 8])
 def test_gemm_decode_many_row_blocks(capi, M):
-    # N/32 >= 1024 row blocks: the 32-row streaming kernel with workgroup-staged
-    # activations (fewer blocks take the 16-row kernel); N not a multiple of 32
+    # many row blocks with N not a multiple of 32 or 16: the last workgroup of
+    # the M <= 8 streaming kernel holds a partial block
     g = rng(4270 + M)
     N, K = 33000, 512
     xq, xs, wq, ws = _rand_operands(g, M, N, K)

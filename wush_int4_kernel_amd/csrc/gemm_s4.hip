@@ -542,8 +542,10 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
 // and are added once at the end.
 constexpr int kStream8ZeroBytes = 1024;         // zero words read by off-diagonal lanes
 
-template <int PF>
-__global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __restrict__ xq,
+// NH = 16-column halves per wavefront (2: 32 weight rows, 1: 16 rows), WPB =
+// wavefronts per workgroup sharing the staged activations.
+template <int PF, int NH, int WPB>
+__global__ __launch_bounds__(64 * WPB) void gemm_s4_stream8_kernel(const uint8_t* __restrict__ xq,
                                                               const uint16_t* __restrict__ xs,
                                                               const uint8_t* __restrict__ wq,
                                                               const uint16_t* __restrict__ ws,
@@ -552,7 +554,11 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
                                                               int M, int N, int K, int groups_per_split) {
     typedef float v4f __attribute__((ext_vector_type(4)));
     typedef short v4s __attribute__((ext_vector_type(4)));
-    constexpr int kSlab = kStreamSG * 2 * kStreamPlane;
+    constexpr int kRows = 16 * NH;               // weight rows per wavefront
+    constexpr int kNW = kRows / 8;               // weight load instructions per stage
+    constexpr int kPlane = kRows * 8 + 16;       // slab plane: kRows x 8 B + pad
+    constexpr int kSlab = kStreamSG * 2 * kPlane;
+    constexpr int kThreads = 64 * WPB;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -568,39 +574,39 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
     uint8_t* x_zero = x_l + (size_t)groups_per_split * 128;          // kStream8ZeroBytes of zeros
     uint8_t* slab = x_zero + kStream8ZeroBytes + (size_t)wave * kSlab;
 
-    const int nb0 = blockIdx.x * 4 + wave;       // 32-row weight block of this wavefront
+    const int nb0 = blockIdx.x * WPB + wave;     // kRows-row weight block of this wavefront
     const size_t slice = (size_t)8 * K2;
     uint32_t wmask = 0;
     {
-        const int nvalid = N - nb0 * 32;
+        const int nvalid = N - nb0 * kRows;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) wmask |= (8 * j + (lane >> 3) < nvalid ? 1u : 0u) << j;
+        for (int j = 0; j < kNW; ++j) wmask |= (8 * j + (lane >> 3) < nvalid ? 1u : 0u) << j;
     }
-    const int n_first = nb0 * 32 + (lane >> 3);
+    const int n_first = nb0 * kRows + (lane >> 3);
     const uint8_t* wp = wq + (size_t)(n_first < N ? n_first : N - 1) * K2 + (size_t)(g_begin + (lane & 7)) * 16;
-    const uint16_t* sp[2];
+    const uint16_t* sp[NH];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int n = nb0 * 32 + 16 * h + r16;
+    for (int h = 0; h < NH; ++h) {
+        const int n = nb0 * kRows + 16 * h + r16;
         sp[h] = ws + (size_t)(n < N ? n : N - 1) * G + g_begin;
     }
 
     struct Stage {
-        uint4 w[4];      // weight line chunks: row 8j + lane/8, group lane%8
-        uint4 sw[2];     // 8 bf16 weight scales of column 16h + r16
+        uint4 w[kNW];    // weight line chunks: row 8j + lane/8, group lane%8
+        uint4 sw[NH];    // 8 bf16 weight scales of column 16h + r16
     };
     const int nst = gcount / kStreamSG;
     auto load = [&](int st, Stage& S) {
         const size_t off = (size_t)st * (kStreamSG * 16);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < kNW; ++j) {
             // rows past N re-read the block's first valid rows; they only feed
             // output columns >= N, which are never stored
             const size_t row_off = ((wmask >> j) & 1u) ? (size_t)j * slice : 0;
             S.w[j] = load_nt16(wp + row_off + off);
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) S.sw[h] = *reinterpret_cast<const uint4*>(sp[h] + st * kStreamSG);
+        for (int h = 0; h < NH; ++h) S.sw[h] = *reinterpret_cast<const uint4*>(sp[h] + st * kStreamSG);
     };
     // weights first: their HBM latency overlaps the staging below
     Stage buf[PF];
@@ -610,7 +616,7 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
     // Stage x scales (as group pairs), activation codes and the zero words.
     {
         const int nchunk = 8 * (gcount >> 3);    // 16-byte loads: 8 groups of one row
-        for (int c = threadIdx.x; c < nchunk; c += 256) {
+        for (int c = threadIdx.x; c < nchunk; c += kThreads) {
             const int m = c & 7, gc = c >> 3;
             const uint4 v = m < M ? *reinterpret_cast<const uint4*>(xs + (size_t)m * G + g_begin + gc * 8)
                                   : make_uint4(0, 0, 0, 0);
@@ -621,11 +627,11 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
         }
         constexpr int U = 8;
         const int nx = gcount * 8;
-        for (int c0 = threadIdx.x; c0 < nx; c0 += 256 * U) {
+        for (int c0 = threadIdx.x; c0 < nx; c0 += kThreads * U) {
             uint4 v[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int c = c0 + u * 256;
+                const int c = c0 + u * kThreads;
                 const int g = c >> 3, m = c & 7;
                 v[u] = (c < nx && m < M)
                            ? *reinterpret_cast<const uint4*>(xq + (size_t)m * K2 + (size_t)(g_begin + g) * 16)
@@ -633,7 +639,7 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int c = c0 + u * 256;
+                const int c = c0 + u * kThreads;
                 if (c < nx) {
                     const int g = c >> 3, m = c & 7;
                     *reinterpret_cast<uint2*>(x_l + (size_t)g * 128 + m * 8) = make_uint2(v[u].x, v[u].y);
@@ -645,7 +651,7 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
             reinterpret_cast<uint4*>(x_zero)[threadIdx.x] = make_uint4(0, 0, 0, 0);
     }
     __syncthreads();
-    if (nb0 * 32 >= N) return;
+    if (nb0 * kRows >= N) return;
 
     // Activation operand: lane (r16 = m + 8e, q) reads half q%2 of group 2p+e
     // of row m when q/2 == e, else a zero word.  Per stage the data lanes
@@ -655,28 +661,28 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
     const uint8_t* x_base = a_data ? x_l + ae * 128 + (q & 1) * 64 + am * 8 : x_zero;
     const int x_step = a_data ? kStreamSG * 128 : 0;
     const uint32_t sx_mask = ae ? 0xffff0000u : 0x0000ffffu;
-    const uint8_t* b_base = slab + q * kStreamPlane + r16 * 8;
+    const uint8_t* b_base = slab + q * kPlane + r16 * 8;
 
-    float acc[2][4];
+    float acc[NH][4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NH; ++h)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[h][j] = 0.0f;
 
     auto process = [&](int st, Stage& S) {
         // 1. transpose this stage's weights into the slab, [group][half][row][8 B]
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < kNW; ++j) {
             const uint4 v = S.w[j];
             const int row = 8 * j + (lane >> 3), g = lane & 7;
             uint8_t* base = slab + row * 8;
-            *reinterpret_cast<uint2*>(base + (g * 2 + 0) * kStreamPlane) = make_uint2(v.x, v.y);
-            *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) = make_uint2(v.z, v.w);
+            *reinterpret_cast<uint2*>(base + (g * 2 + 0) * kPlane) = make_uint2(v.x, v.y);
+            *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kPlane) = make_uint2(v.z, v.w);
         }
         // 2. per group pair p: one activation operand, two 16-column halves,
         //    software pipelined (pair p+1's MFMAs before pair p's fold)
         const uint8_t* xa = x_base + (size_t)st * x_step;
-        auto issue = [&](int p, v4i (&d)[2], v4f (&sc)[2]) {
+        auto issue = [&](int p, v4i (&d)[NH], v4f (&sc)[NH]) {
             const uint2 xw = *reinterpret_cast<const uint2*>(xa + p * 256);
             uint32_t a0, a1, a2, a3;
             unpack_s4x8_x16(xw.x, a0, a1);
@@ -685,8 +691,8 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
             const uint32_t sxa = sx_l[(st * 4 + p) * 8 + am] & sx_mask;
             const uint2 sa2 = (p & 1) ? make_uint2(0u, sxa) : make_uint2(sxa, 0u);
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint2 w = *reinterpret_cast<const uint2*>(b_base + p * 4 * kStreamPlane + h * 128);
+            for (int h = 0; h < NH; ++h) {
+                const uint2 w = *reinterpret_cast<const uint2*>(b_base + p * 4 * kPlane + h * 128);
                 uint32_t b0, b1, b2, b3;
                 unpack_s4x8_x16(w.x, b0, b1);
                 unpack_s4x8_x16(w.y, b2, b3);
@@ -698,14 +704,14 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
                                                                    (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
             }
         };
-        auto fold = [&](const v4i (&d)[2], const v4f (&sc)[2]) {
+        auto fold = [&](const v4i (&d)[NH], const v4f (&sc)[NH]) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < NH; ++h)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[h][j] = __builtin_fmaf((float)d[h][j], sc[h][j], acc[h][j]);
         };
-        v4i d0[2], d1[2];
-        v4f s0[2], s1[2];
+        v4i d0[NH], d1[NH];
+        v4f s0[NH], s1[NH];
         issue(0, d0, s0);
         issue(1, d1, s1);
         fold(d0, s0);
@@ -732,8 +738,8 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
     // even-group sums (lanes 0-31) + odd-group sums (lanes 32-63); lanes 0-31
     // then hold rows m = 4q + j of columns 16h + r16
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int col = nb0 * 32 + 16 * h + r16;
+    for (int h = 0; h < NH; ++h) {
+        const int col = nb0 * kRows + 16 * h + r16;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float v = (acc[h][j] + __shfl_xor(acc[h][j], 32)) * kFold8OutScale;
@@ -744,175 +750,6 @@ __global__ __launch_bounds__(256) void gemm_s4_stream8_kernel(const uint8_t* __r
                 else
                     y[(size_t)row * N + col] = f32_to_f16_bits(v);
             }
-        }
-    }
-}
-
-// ----------------------------------- streaming kernel, M <= 8, 16-row waves
-// The MFMA scheme of gemm_s4_stream8_kernel (16x16x64 int8 over a group pair
-// with a block-diagonal activation operand, fold factors from a 16x16x16
-// bf16 MFMA), but each wavefront owns 16 weight rows -- twice the
-// wavefronts for the same N, which is what keeps HBM busy: a load-only probe
-// of this stream reads 6.1 TB/s with 16-row wavefronts against 5.4 TB/s with
-// 32-row ones -- and nothing is staged per workgroup: every stage of 8 groups
-// brings, per wavefront, 16 rows x 128 B of weights (2 load instructions),
-// the 8 activation rows' codes of those groups (1 instruction, L2-resident)
-// and both scale slices in registers, and goes through a wavefront-private
-// LDS slab (weights [group][half][row][8 B], activations [group][half][m][8 B]).
-// Off-diagonal activation lanes read a shared block of zero words.  No
-// workgroup barrier is needed after the zero fill.
-constexpr int kS16WPlane = 16 * 8 + 16;          // weight slab plane: 16 rows x 8 B + pad
-constexpr int kS16XPlane = 8 * 8 + 8;            // activation slab plane: 8 rows x 8 B + pad
-constexpr int kS16Slab = kStreamSG * 2 * (kS16WPlane + kS16XPlane);
-constexpr int kS16Zero = 1024;                   // zero words (pairs 0..3 at 4 * kS16XPlane each)
-constexpr int kS16Waves = 4;
-
-template <int PF>
-__global__ __launch_bounds__(256) void gemm_s4_stream16_kernel(const uint8_t* __restrict__ xq,
-                                                               const uint16_t* __restrict__ xs,
-                                                               const uint8_t* __restrict__ wq,
-                                                               const uint16_t* __restrict__ ws,
-                                                               uint16_t* __restrict__ y,
-                                                               float* __restrict__ partial,
-                                                               int M, int N, int K, int groups_per_split) {
-    typedef float v4f __attribute__((ext_vector_type(4)));
-    typedef short v4s __attribute__((ext_vector_type(4)));
-    __shared__ __align__(16) uint8_t lds[kS16Zero + kS16Waves * kS16Slab];
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int q = lane >> 4;                     // MFMA lane block: k 16q..16q+15 of the pair
-    const int r16 = lane & 15;                   // MFMA row (A: m + 8e) / column (B: n)
-    const int G = K >> 5;
-    const int K2 = K >> 1;
-    const int g_begin = blockIdx.y * groups_per_split;
-    const int g_end = min(G, g_begin + groups_per_split);
-    const int nst = (g_end - g_begin) / kStreamSG;
-    uint8_t* zero = lds;
-    uint8_t* wslab = lds + kS16Zero + wave * kS16Slab;
-    uint8_t* xslab = wslab + kStreamSG * 2 * kS16WPlane;
-
-    if (threadIdx.x < kS16Zero / 16) reinterpret_cast<uint4*>(zero)[threadIdx.x] = make_uint4(0, 0, 0, 0);
-    __syncthreads();
-
-    const int n0 = (blockIdx.x * kS16Waves + wave) * 16;
-    if (n0 >= N) return;
-    // weight loads: lane -> row n0 + 8j + lane/8, 16-byte chunk lane%8 of the stage
-    const int wrow = lane >> 3, wg = lane & 7;
-    const uint8_t* wp[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = n0 + 8 * j + wrow;
-        wp[j] = wq + (size_t)(n < N ? n : N - 1) * K2 + (size_t)(g_begin + wg) * 16;
-    }
-    // activation loads: lane -> row m = lane/8 (rows >= M repeat row M-1: not stored), group lane%8
-    const int xm = lane >> 3;
-    const uint8_t* xp = xq + (size_t)(xm < M ? xm : M - 1) * K2 + (size_t)(g_begin + wg) * 16;
-    // scale loads: 8 groups of weight row n0 + r16 and of activation row r16 % 8
-    const int sn = n0 + r16;
-    const uint16_t* swp = ws + (size_t)(sn < N ? sn : N - 1) * G + g_begin;
-    const int sm = r16 & 7;
-    const uint16_t* sxp = xs + (size_t)(sm < M ? sm : M - 1) * G + g_begin;
-
-    struct Stage {
-        uint4 w[2];
-        uint4 x;
-        uint4 sw;        // bf16 pairs (2p, 2p+1) of column r16
-        uint4 sx;        // bf16 pairs (2p, 2p+1) of activation row r16 % 8
-    };
-    auto load = [&](int st, Stage& S) {
-        const size_t off = (size_t)st * (kStreamSG * 16);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) S.w[j] = load_nt16(wp[j] + off);
-        S.x = *reinterpret_cast<const uint4*>(xp + off);
-        S.sw = *reinterpret_cast<const uint4*>(swp + st * kStreamSG);
-        S.sx = *reinterpret_cast<const uint4*>(sxp + st * kStreamSG);
-    };
-
-    // MFMA operand addresses.  A: lane (m + 8e, q) holds half q%2 of group
-    // 2p+e of activation row m when q/2 == e, else zeros.
-    const int am = r16 & 7, ae = r16 >> 3;
-    const bool a_data = (q >> 1) == ae;
-    const uint8_t* a_rd = a_data ? xslab + (2 * ae + (q & 1)) * kS16XPlane + am * 8 : zero;
-    const uint32_t sx_mask = ae ? 0xffff0000u : 0x0000ffffu;
-    // B: lane (n, q) holds half q%2 of group 2p + q/2 of weight row n.
-    const uint8_t* b_rd = wslab + q * kS16WPlane + r16 * 8;
-
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto process = [&](Stage& S) {
-        // transpose the stage into the slabs
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            uint8_t* b = wslab + (8 * j + wrow) * 8;
-            *reinterpret_cast<uint2*>(b + (wg * 2 + 0) * kS16WPlane) = make_uint2(S.w[j].x, S.w[j].y);
-            *reinterpret_cast<uint2*>(b + (wg * 2 + 1) * kS16WPlane) = make_uint2(S.w[j].z, S.w[j].w);
-        }
-        {
-            uint8_t* b = xslab + xm * 8;
-            *reinterpret_cast<uint2*>(b + (wg * 2 + 0) * kS16XPlane) = make_uint2(S.x.x, S.x.y);
-            *reinterpret_cast<uint2*>(b + (wg * 2 + 1) * kS16XPlane) = make_uint2(S.x.z, S.x.w);
-        }
-        auto issue = [&](int p, v4i& d, v4f& sc) {
-            const uint2 xw = *reinterpret_cast<const uint2*>(a_rd + p * 4 * kS16XPlane);
-            uint32_t a0, a1, a2, a3;
-            unpack_s4x8_x16(xw.x, a0, a1);
-            unpack_s4x8_x16(xw.y, a2, a3);
-            const v4i A = {(int)a0, (int)a1, (int)a2, (int)a3};
-            const uint2 ww = *reinterpret_cast<const uint2*>(b_rd + p * 4 * kS16WPlane);
-            uint32_t b0, b1, b2, b3;
-            unpack_s4x8_x16(ww.x, b0, b1);
-            unpack_s4x8_x16(ww.y, b2, b3);
-            const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
-            const uint32_t sxa = (&S.sx.x)[p] & sx_mask;
-            const uint2 sa2 = (p & 1) ? make_uint2(0u, sxa) : make_uint2(sxa, 0u);
-            const uint2 sb2 = (p < 2) ? make_uint2(S.sw.x, S.sw.y) : make_uint2(S.sw.z, S.sw.w);
-            d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i){0, 0, 0, 0}, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s, sa2), __builtin_bit_cast(v4s, sb2),
-                                                           (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-        };
-        auto fold = [&](const v4i& d, const v4f& sc) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf((float)d[j], sc[j], acc[j]);
-        };
-        v4i d0, d1;
-        v4f s0, s1;
-        issue(0, d0, s0);
-        issue(1, d1, s1);
-        fold(d0, s0);
-        issue(2, d0, s0);
-        fold(d1, s1);
-        issue(3, d1, s1);
-        fold(d0, s0);
-        fold(d1, s1);
-    };
-
-    Stage buf[PF];
-#pragma unroll
-    for (int d = 0; d < PF; ++d) load(min(d, nst - 1), buf[d]);
-    int st = 0;
-    for (; st + PF <= nst; st += PF) {
-#pragma unroll
-        for (int d = 0; d < PF; ++d) {
-            process(buf[d]);
-            load(min(st + d + PF, nst - 1), buf[d]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-#pragma unroll
-    for (int d = 0; d < PF - 1; ++d)
-        if (st + d < nst) process(buf[d]);
-
-    // even-group sums (lanes 0-31) + odd-group sums (lanes 32-63); lanes 0-31
-    // then hold rows m = 4q + j of column n0 + r16
-    const int col = n0 + r16;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float v = (acc[j] + __shfl_xor(acc[j], 32)) * kFold8OutScale;
-        const int row = 4 * q + j;
-        if (lane < 32 && row < M && col < N) {
-            if (partial != nullptr)
-                partial[((size_t)blockIdx.y * M + row) * N + col] = v;
-            else
-                y[(size_t)row * N + col] = f32_to_f16_bits(v);
         }
     }
 }
@@ -984,20 +821,23 @@ constexpr size_t kStreamLdsMax = 64 * 1024;
 // LDS bytes of a streaming launch with gps groups per slice: M <= 8 stages
 // x scales (4 B per group pair and row) and codes (128 B per group) plus the
 // zero words; M > 8 stages bf16 x scales of 32 rows.  Plus the four slabs.
-// M <= 8 with few 32-row blocks (N/32 below the wavefront target) streams
-// 16 rows per wavefront (gemm_s4_stream16_kernel) instead of splitting K; with
-// many blocks the 32-row kernel, whose activations are staged once per
-// workgroup, is faster (measured: Q8 M=1 14.4 vs 18.7 us, L70 M=8 63.7 vs
-// 58.1 us).
-#ifndef WUSH_STREAM16
-#define WUSH_STREAM16 1
+// Geometry of the M <= 8 kernel: 16 weight rows per wavefront (twice the
+// wavefronts of 32-row ones, which keeps more HBM requests in flight) and 8
+// wavefronts per workgroup sharing the staged activations.  Measured at L70:
+// 55.7 us (16 rows, 8 waves), 58.2 (32 rows, 4 waves), 63.0 (16 rows, 4
+// waves: 3 workgroups per CU do not hold 14 wavefronts); at Q8 it also beats
+// split-K (14.6 vs 18.7 us at M=1).
+#ifndef WUSH_S8_NH
+#define WUSH_S8_NH 1             // 16-column halves per wavefront of the M <= 8 kernel
 #endif
-static bool use_stream16(int64_t M, int64_t N) {
-    return WUSH_STREAM16 && M <= 8 && (N + 31) / 32 < WUSH_STREAM_WAVES;
-}
-static size_t stream_smem(int64_t gps, bool m8, bool s16) {
-    if (s16) return 0;                       // static LDS only
-    if (m8) return (size_t)gps * (16 + 128) + kStream8ZeroBytes + 4 * (size_t)kStreamSG * 2 * kStreamPlane;
+#ifndef WUSH_S8_WPB
+#define WUSH_S8_WPB 8            // its wavefronts per workgroup
+#endif
+constexpr int kS8Rows = 16 * WUSH_S8_NH;
+static size_t stream_smem(int64_t gps, bool m8) {
+    if (m8)
+        return (size_t)gps * (16 + 128) + kStream8ZeroBytes +
+               (size_t)WUSH_S8_WPB * kStreamSG * 2 * (kS8Rows * 8 + 16);
     return (size_t)gps * 32 * sizeof(uint16_t) + 4 * (size_t)kStreamNB * kStreamSG * 2 * kStreamPlane;
 }
 
@@ -1018,9 +858,8 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         // streaming kernel: one wavefront per 32*kStreamNB weight rows
         p.cfg = 3; p.tm = 32; p.tn = 4 * kStreamNB * 32; p.sg = kStreamSG;
         p.mr = (int)((M + 7) / 8 * 8);
-        const bool s16 = use_stream16(M, N);
-        const int rows_per_wave = s16 ? 16 : 32 * kStreamNB;
-        p.tn = 4 * rows_per_wave;
+        const int rows_per_wave = M <= 8 ? kS8Rows : 32 * kStreamNB;
+        p.tn = (M <= 8 ? WUSH_S8_WPB : 4) * rows_per_wave;
         const int64_t waves = (N + rows_per_wave - 1) / rows_per_wave;
         static_assert(kStreamNB == 1, "the M <= 8 kernel streams one 32-row block per wavefront");
         int s = 1;
@@ -1028,14 +867,14 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         int64_t gps = (G0 + s - 1) / s;
         gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
         const bool m8 = p.mr == 8;
-        while (stream_smem(gps, m8, s16) > kStreamLdsMax && gps > kStreamSG) {
+        while (stream_smem(gps, m8) > kStreamLdsMax && gps > kStreamSG) {
             s *= 2;
             gps = (G0 + s - 1) / s;
             gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
         }
         s = (int)((G0 + gps - 1) / gps);
         const bool ws_ok = s == 1 || (size_t)s * (size_t)M * (size_t)N * sizeof(float) <= ws_bytes_available;
-        if (ws_ok && stream_smem(gps, m8, s16) <= kStreamLdsMax) {
+        if (ws_ok && stream_smem(gps, m8) <= kStreamLdsMax) {
             p.splits = s;
             p.groups_per_split = (int)gps;
             return p;
@@ -1093,15 +932,12 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     const int m = (int)M, n = (int)N, k = (int)K;
     if (p.cfg == 3) {
         if constexpr (!PT) {
-            const bool s16 = p.tn == 64;
-            const size_t smem = stream_smem(p.groups_per_split, p.mr == 8, s16);
+            const size_t smem = stream_smem(p.groups_per_split, p.mr == 8);
             dim3 grid((unsigned)((N + p.tn - 1) / p.tn), (unsigned)p.splits);
             switch (p.mr) {
                 case 8:
-                    if (s16)
-                        gemm_s4_stream16_kernel<kStreamPFX><<<grid, 256, 0, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
-                    else
-                        gemm_s4_stream8_kernel<kStreamPFX><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
+                    gemm_s4_stream8_kernel<kStreamPFX, WUSH_S8_NH, WUSH_S8_WPB><<<grid, 64 * WUSH_S8_WPB, smem, stream>>>(
+                        xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
                     break;
                 case 16: gemm_s4_stream_kernel<16, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
                 case 24: gemm_s4_stream_kernel<24, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
