@@ -12,10 +12,12 @@ synthetic activations, exactly as the reference's official bench chains it
   M <= 32: fused_transform_quant_int4_smallm -> w4a4_gemm_s4
   else   : fused_transform_quant_int4_v3     -> w4a4_gemm_s4
 with the weights pre-quantized (W' = W T^-1, sigma-clip s4 + bf16 scales) and
-resident in HBM.  One HIP graph holds one chain per distinct weight copy (the copies together
-exceed the 256 MB MALL, so every step streams its weights from HBM), the way a
-model's layer stack is captured; replays are timed and divided by the number of
-steps they hold.  `value` is the M=1 layer time (the
+resident in HBM.  One HIP graph holds --graph-steps chains (12 by default), each on
+its own layer's weights and transform, cycling over --copies distinct weight copies
+(together they exceed the 256 MB MALL, so every step streams its weights from HBM),
+the way a model's decoder stack is captured in one graph; replays are timed and
+divided by the number of steps they hold, so the per-replay launch cost (about
+5 us on this part) is paid once per graph as in a model's decode step.  `value` is the M=1 layer time (the
 headline decode point); the other M are reported beside it, each with the
 hipBLASLt bf16 GEMM time at the same shape measured the same way.
 
@@ -59,6 +61,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--ms", default="1,8,32,4096", help="comma-separated M values")
     ap.add_argument("--copies", type=int, default=3, help="distinct weight copies (MALL defeat)")
+    ap.add_argument("--graph-steps", type=int, default=12, help="layer steps captured in one HIP graph")
     ap.add_argument("--no-blas", action="store_true", help="skip the hipBLASLt bf16 baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--K", type=int, default=K_L70)
@@ -129,20 +132,20 @@ def main():
     wq, ws = _C.quant_int4(Wt)
     del W, Xcal
     torch.cuda.synchronize()
-    copies = [(wq, ws)] + [(wq.clone(), ws.clone()) for _ in range(args.copies - 1)]
+    copies = [(wq, ws, T)] + [(wq.clone(), ws.clone(), T.clone()) for _ in range(args.copies - 1)]
     log(f"[bench] weights ready: N={N} K={K}, {args.copies} copies x "
         f"{(wq.numel() + ws.numel() * 2) / 1e6:.1f} MB ({time.time() - t0:.1f}s)")
 
     stream = torch.cuda.current_stream()
 
-    def chain_fn(X, wq_, ws_, M):
+    def chain_fn(X, wq_, ws_, T_, M):
         # the reference's dispatch by M (bench/exp_p13_official.py:31-39)
-        return make_chain(X, T, wq_, ws_, M)
+        return make_chain(X, T_, wq_, ws_, M)
 
     def capture(fns):
-        """One HIP graph holding one layer step per function (one per weight
-        copy), the way a model's decoder stack is captured: the per-replay
-        launch overhead is paid once per len(fns) steps."""
+        """One HIP graph holding one layer step per function, the way a
+        model's decoder stack is captured: the per-replay launch overhead is
+        paid once per len(fns) steps."""
         for _ in range(2):
             for fn in fns:
                 fn()
@@ -171,7 +174,7 @@ def main():
         xq, xs = _C.fused_transform_quant_int4_smallm(X, T)
         y = torch.empty(M, N, dtype=torch.float16, device=dev)
         for i in range(args.warmup + args.steps):
-            cq, cs = copies[i % len(copies)]
+            cq, cs, _ = copies[i % len(copies)]
             capi.gemv_int4(xq.data_ptr(), xs.data_ptr(), cq.data_ptr(), cs.data_ptr(), y.data_ptr(),
                            M, N, K, stream.cuda_stream)
         torch.cuda.synchronize()
@@ -191,10 +194,11 @@ def main():
     blas_w = None
     for M in Ms:
         X = activations(M, gdev).to(torch.bfloat16).contiguous()
-        graph = capture([chain_fn(X, cq, cs, M) for cq, cs in copies])
+        gsteps = [copies[i % len(copies)] for i in range(args.graph_steps)]
+        graph = capture([chain_fn(X, cq, cs, Tc, M) for cq, cs, Tc in gsteps])
         steps = args.steps if M <= 64 else max(10, args.steps // 10)
         warm = args.warmup if M <= 64 else max(3, args.warmup // 4)
-        t_int4 = time_graph(graph, len(copies), steps, warm)
+        t_int4 = time_graph(graph, args.graph_steps, steps, warm)
         del graph
         entry = {
             "us": round(t_int4 * 1e6, 2),
@@ -210,8 +214,9 @@ def main():
             if blas_w is None:
                 blas_w = [Wt] + [Wt.clone() for _ in range(1)]
             Xb = X
-            bgraph = capture([lambda Wc=Wc: torch.matmul(Xb, Wc.t()) for Wc in blas_w])
-            t_blas = time_graph(bgraph, len(blas_w), steps, warm)
+            bgraph = capture([lambda Wc=blas_w[i % len(blas_w)]: torch.matmul(Xb, Wc.t())
+                              for i in range(args.graph_steps)])
+            t_blas = time_graph(bgraph, args.graph_steps, steps, warm)
             del bgraph
             entry["hipblaslt_bf16_us"] = round(t_blas * 1e6, 2)
             entry["speedup_vs_hipblaslt"] = round(t_blas / t_int4, 3)
@@ -265,7 +270,7 @@ def main():
     launches = max(50, args.steps)
 
     def launch(i):
-        cq, cs = copies[i % len(copies)]
+        cq, cs, _ = copies[i % len(copies)]
         capi.gemv_int4(xq.data_ptr(), xs.data_ptr(), cq.data_ptr(), cs.data_ptr(), y.data_ptr(),
                        M, N, K, stream.cuda_stream)
 
@@ -318,7 +323,8 @@ def main():
                 "transformed by this build's WUSH T and sigma-clip quantized",
         "config": {
             "workload": f"Llama-70B FFN layer K={K} N={N}, M=1: fused_transform_quant_int4_smallm + w4a4_gemv, "
-                        f"one HIP graph of {args.copies} layer steps over distinct weight copies",
+                        f"one HIP graph of {args.graph_steps} layer steps cycling over {args.copies} "
+                        f"distinct weight copies",
             "K": K, "N": N, "M": 1,
         },
         "layers": layers,

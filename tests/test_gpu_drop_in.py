@@ -204,6 +204,25 @@ def test_gemv_ops(C):
         C.w4a4_gemv_multi(xq, xs, wq, ws)
 
 
+@pytest.mark.parametrize("M", [1, 2, 5, 6, 7, 8])
+def test_decode_ops_route_to_either_kernel(C, M):
+    # w4a4_gemm_s4 and w4a4_gemv_multi pick the dot8 GEMV or the MFMA GEMM by
+    # (M, N*K): small weights at M 7-8 take the GEMM, N*K >= 2^28 the GEMV.
+    # Either way the result is the same product (checked on sampled columns).
+    import torch
+    g = rng(60 + M)
+    for N, K in [(4096, 4096), (32768, 8192)]:
+        wq, ws = C.quant_int4(to_dev_bf16(_bf16(g, (N, K), 0.02)))
+        xq, xs = C.quant_int4(to_dev_bf16(_bf16(g, (M, K))))
+        cols = torch.from_numpy(np.sort(g.choice(N, size=512, replace=False))).cuda()
+        ref = oracle.gemm_f64(xq.cpu().numpy(), bf16_tensor_bits(xs), wq[cols].cpu().numpy(),
+                              bf16_tensor_bits(ws[cols]))
+        y1 = C.w4a4_gemm_s4(xq, xs, wq, ws)
+        y2 = C.w4a4_gemv_multi(xq, xs, wq, ws)
+        assert torch.equal(y1, y2), (M, N, K)
+        assert rel_fro(f16_tensor_f64(y1[:, cols]), ref) < 2e-3, (M, N, K)
+
+
 def test_s4_atom_selftest(C):
     import torch
     g = rng(7)

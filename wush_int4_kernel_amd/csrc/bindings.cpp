@@ -103,12 +103,31 @@ void check_packed(const torch::Tensor& xq, const torch::Tensor& xs, const torch:
     TORCH_CHECK(xs.is_cuda() && ws.is_cuda(), "tensors must be CUDA");
 }
 
-// Shared GEMM launch: y (M, N) fp16 = group-scaled product.
-torch::Tensor gemm_2d(const torch::Tensor& xq2, const torch::Tensor& xs2, const torch::Tensor& wq,
-                      const torch::Tensor& ws, int64_t K, const char* op) {
+// Which kernel family computes a product with M activation rows.  Both give
+// the same math (exact int32 group dots folded in fp32).  Measured on MI355X:
+// the dot8 streaming GEMV (wush_gemv_int4) is faster than the int8-MFMA
+// streaming GEMM (wush_gemm_s4) up to M = 6 at every shape measured (Llama-70B
+// FFN K=8192 N=57344 M=4: 43.6 vs 54.9 us; Qwen3-8B K=4096 N=24576 M=6: 14.0
+// vs 14.8 us) and up to M = 8 once the weights are large (N*K >= 2^28;
+// Llama-70B M=8: 53.0 vs 56.2 us, Qwen3-8B M=8: 17.2 vs 15.0 us).  The GEMV
+// stages M*K*(1/2 + 1/8) bytes of activations in LDS, at most 64 KiB.
+bool gemv_preferred(int64_t M, int64_t N, int64_t K) {
+    const bool lds_fits = M * (K / 2) + M * (K / 32) * 4 <= 64 * 1024;
+    return lds_fits && M >= 1 && (M <= 6 || (M <= 8 && N * K >= (int64_t(1) << 28)));
+}
+
+// Shared product launch: y (M, N) fp16 = group-scaled product.
+torch::Tensor product_2d(const torch::Tensor& xq2, const torch::Tensor& xs2, const torch::Tensor& wq,
+                         const torch::Tensor& ws, int64_t K, const char* op) {
     const int64_t M = xq2.size(0), N = wq.size(0);
     const at::hip::OptionalHIPGuardMasqueradingAsCUDA guard(xq2.device());
     auto y = torch::empty({M, N}, torch::dtype(torch::kHalf).device(xq2.device()));
+    if (gemv_preferred(M, N, K)) {
+        check_status(wush_gemv_int4(ptr<uint8_t>(xq2), ptr<uint16_t>(xs2), ptr<uint8_t>(wq), ptr<uint16_t>(ws),
+                                    ptr<uint16_t>(y), M, N, K, current_stream(xq2)),
+                     op);
+        return y;
+    }
     const size_t wsb = wush_gemm_s4_workspace_bytes(M, N, K);
     torch::Tensor work;
     if (wsb) work = torch::empty({(int64_t)wsb}, torch::dtype(torch::kUInt8).device(xq2.device()));
@@ -130,7 +149,7 @@ torch::Tensor w4a4_gemm_s4(torch::Tensor xq, torch::Tensor xs, torch::Tensor wq,
     TORCH_CHECK(wq.dim() == 2 && wq.size(1) == K2 && ws.size(-1) == G && ws.numel() == wq.size(0) * G,
                 "K mismatch");
     TORCH_CHECK(xs2.size(0) == xq2.size(0), "K mismatch");
-    return gemm_2d(xq2, xs2, wq, ws, K, "w4a4_gemm_s4");
+    return product_2d(xq2, xs2, wq, ws, K, "w4a4_gemm_s4");
 }
 
 // w4a4_gemm (csrc/gemm_int4.cu:89-130): y keeps xq's leading dims, (..., N).
@@ -143,7 +162,7 @@ torch::Tensor w4a4_gemm(torch::Tensor xq, torch::Tensor xs, torch::Tensor wq, to
                 "K mismatch between x/w tensors");
     auto xq2 = xq.view({-1, K2});
     auto xs2 = xs.reshape({-1, G});
-    auto y = gemm_2d(xq2, xs2, wq, ws, K, "w4a4_gemm");
+    auto y = product_2d(xq2, xs2, wq, ws, K, "w4a4_gemm");
     return y.view(with_last(xq, wq.size(0)));
 }
 
@@ -153,7 +172,7 @@ torch::Tensor w4a4_gemm_v1(torch::Tensor xq, torch::Tensor xs, torch::Tensor wq,
     const int64_t K2 = xq.size(-1);
     const int64_t K = K2 * 2, G = K / 32;
     TORCH_CHECK(K % 32 == 0 && wq.dim() == 2 && wq.size(1) == K2 && ws.size(-1) == G, "K mismatch");
-    return gemm_2d(xq.reshape({-1, K2}), xs.reshape({-1, G}), wq, ws, K, "w4a4_gemm_v1");
+    return product_2d(xq.reshape({-1, K2}), xs.reshape({-1, G}), wq, ws, K, "w4a4_gemm_v1");
 }
 
 // w4a4_gemm_v2 (csrc/gemm_wmma2.cu:141-181): y (M, N), K % 64 == 0.
@@ -163,36 +182,7 @@ torch::Tensor w4a4_gemm_v2(torch::Tensor xq, torch::Tensor xs, torch::Tensor wq,
     const int64_t K = K2 * 2, G = K / 32;
     TORCH_CHECK(K % 64 == 0, "K must be multiple of 64");
     TORCH_CHECK(wq.dim() == 2 && wq.size(1) == K2 && ws.size(-1) == G, "K mismatch");
-    return gemm_2d(xq.reshape({-1, K2}), xs.reshape({-1, G}), wq, ws, K, "w4a4_gemm_v2");
-}
-
-// Decode product for 1 <= M <= 8.  M <= 5 runs the dot8 streaming GEMV;
-// from M = 6 the int8-MFMA streaming GEMM is faster (its fold work grows with M
-// more slowly than 4 dot8 + 3 fold ops per row and group), and shapes whose
-// activations the GEMV cannot stage in LDS also go to the GEMM.  Both compute
-// the same product: exact int32 group dots folded in fp32.
-constexpr int64_t kGemvMaxM = 5;
-
-torch::Tensor gemv_impl(const torch::Tensor& xq2, const torch::Tensor& xs2, const torch::Tensor& wq,
-                        const torch::Tensor& ws, int64_t M, int64_t K, const char* op) {
-    const int64_t N = wq.size(0);
-    const at::hip::OptionalHIPGuardMasqueradingAsCUDA guard(xq2.device());
-    auto y = torch::empty({M, N}, torch::dtype(torch::kHalf).device(xq2.device()));
-    const bool lds_fits = M * (K / 2) + M * (K / 32) * 4 <= 64 * 1024;
-    int st = (int)hipErrorInvalidValue;
-    if (M <= kGemvMaxM && lds_fits)
-        st = wush_gemv_int4(ptr<uint8_t>(xq2), ptr<uint16_t>(xs2), ptr<uint8_t>(wq), ptr<uint16_t>(ws),
-                            ptr<uint16_t>(y), M, N, K, current_stream(xq2));
-    if (st == (int)hipErrorInvalidValue && (M > kGemvMaxM || !lds_fits)) {
-        const size_t wsb = wush_gemm_s4_workspace_bytes(M, N, K);
-        torch::Tensor work;
-        if (wsb) work = torch::empty({(int64_t)wsb}, torch::dtype(torch::kUInt8).device(xq2.device()));
-        st = wush_gemm_s4(ptr<uint8_t>(xq2), ptr<uint16_t>(xs2), ptr<uint8_t>(wq), ptr<uint16_t>(ws),
-                          ptr<uint16_t>(y), M, N, K, wsb ? work.data_ptr() : nullptr, wsb,
-                          current_stream(xq2));
-    }
-    check_status(st, op);
-    return y;
+    return product_2d(xq.reshape({-1, K2}), xs.reshape({-1, G}), wq, ws, K, "w4a4_gemm_v2");
 }
 
 // w4a4_gemv (csrc/gemv_int4.cu:191-223): single row, y (N,) fp16.
@@ -203,7 +193,7 @@ torch::Tensor w4a4_gemv(torch::Tensor xq, torch::Tensor xs, torch::Tensor wq, to
     const int64_t K = K2 * 2, G = K / 32;
     TORCH_CHECK(K % 32 == 0 && wq.dim() == 2 && wq.size(1) == K2 && ws.size(-1) == G && xs.numel() == G,
                 "K mismatch");
-    auto y = gemv_impl(xq.reshape({1, K2}), xs.reshape({1, G}), wq, ws, 1, K, "w4a4_gemv");
+    auto y = product_2d(xq.reshape({1, K2}), xs.reshape({1, G}), wq, ws, K, "w4a4_gemv");
     return y.view({wq.size(0)});
 }
 
@@ -218,7 +208,7 @@ torch::Tensor w4a4_gemv_multi(torch::Tensor xq, torch::Tensor xs, torch::Tensor 
     TORCH_CHECK(M >= 1 && M <= 8, "gemv_multi expects 1<=M<=8");
     TORCH_CHECK(K % 32 == 0 && wq.dim() == 2 && wq.size(1) == K2 && ws.size(-1) == G && xs2.size(0) == M,
                 "K mismatch");
-    return gemv_impl(xq2, xs2, wq, ws, M, K, "w4a4_gemv_multi");
+    return product_2d(xq2, xs2, wq, ws, K, "w4a4_gemv_multi");
 }
 
 // s4_atom_selftest (csrc/gemm_s4.cu:74-82): c (8, 8) int32 = a (8, 32) @ b (32, 8).

@@ -9,17 +9,39 @@
 // instruction of a wavefront reads 1 KiB of contiguous codes (16 B per lane)
 // and 128 B of contiguous scales.  The group dot is 4 v_dot8_i32_i4 on the
 // packed nibbles as stored (element 2k low nibble pairs with element 2k low
-// nibble), the fold is one cvt + one mul + one fma in fp32, and a DPP
-// wavefront reduction (VALU only) finishes each output.  Two weight rows are in flight per
-// wavefront so that each lane keeps 2 x (K/2048) 16-byte loads outstanding.
+// nibble), the fold is one cvt + one mul + one fma in fp32.  A chunk of R
+// weight rows (R = 1 at M = 1, else 2) is reduced over the wavefront at once:
+// the R x M partial sums go through a recursive-halving reduction (permlane
+// swaps and DPP, VALU only) that costs about two operations per output.  The
+// next chunk is requested before the current one is reduced, so each lane
+// keeps 2 x R x (K/2048) 16-byte loads outstanding.
 #include "wush_device.h"
 #include "../../include/wush_int4.h"
 
 namespace wush {
 
-constexpr int kGemvWaves = 4;
+// Tuning knobs (defaults measured at K=8192 N=57344 and K=4096 N=24576).
+#ifndef WUSH_GEMV_WAVES
+#define WUSH_GEMV_WAVES 4       // wavefronts per workgroup (2 / 8 / 16 measured no better)
+#endif
+constexpr int kGemvWaves = WUSH_GEMV_WAVES;
+#ifndef WUSH_GEMV_RS
+#define WUSH_GEMV_RS 1          // recursive-halving reduction of the R x M outputs
+#endif
+#ifndef WUSH_GEMV_TBAR
+#define WUSH_GEMV_TBAR 1        // scheduling barrier after each group (fewer live VGPRs)
+#endif
 #ifndef WUSH_GEMV_R1
 #define WUSH_GEMV_R1 1          // weight rows per chunk at M = 1 (measured best)
+#endif
+#ifndef WUSH_GEMV_R2
+#define WUSH_GEMV_R2 2          // ... at M = 2
+#endif
+#ifndef WUSH_GEMV_R4
+#define WUSH_GEMV_R4 2          // ... at M = 3, 4
+#endif
+#ifndef WUSH_GEMV_R8
+#define WUSH_GEMV_R8 2          // ... at M = 5 .. 8
 #endif
 
 __device__ __forceinline__ int dot32_s4(const uint4& a, const uint4& b) {
@@ -43,8 +65,45 @@ struct GemvChunk {
     uint32_t s[R][GPL];
 };
 
+constexpr int pow2_ceil(int v) { return v <= 1 ? 1 : 2 * pow2_ceil((v + 1) / 2); }
+
+// Reduce the R x M per-lane partial sums over the wavefront and store the
+// fp16 outputs of rows n0 .. n0+R-1.  All reductions happen before the one
+// store branch (a store branch per output lets the compiler sink later
+// outputs' dot products past it and keep every group's activations live).
+template <int M, int R>
+__device__ __forceinline__ void store_outputs(const float (&acc)[R][M], int lane, int n0, int n_end, int N,
+                                              uint16_t* __restrict__ y) {
+#if WUSH_GEMV_RS
+    constexpr int V = pow2_ceil(R * M);
+    if constexpr (V > 1) {
+        float v[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[i] = i < R * M ? acc[i / M][i % M] : 0.0f;
+        const float total = wave_reduce_scatter<V>(v, lane);
+        const int idx = wave_rs_index<V>(lane);
+        const int r = idx / M, m = idx % M;
+        if ((lane & (64 / V - 1)) == 0 && idx < R * M && n0 + r < n_end)
+            y[(size_t)m * N + n0 + r] = f32_to_f16_bits(total);
+        return;
+    }
+#endif
+    float v[R][M];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) v[r][m] = wave_sum_dpp(acc[r][m]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+                if (n0 + r < n_end) y[(size_t)m * N + n0 + r] = f32_to_f16_bits(v[r][m]);
+    }
+}
+
 template <int M, int R, int GPL>
-__global__ __launch_bounds__(256) void gemv_int4_kernel(const uint8_t* __restrict__ xq,
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_int4_kernel(const uint8_t* __restrict__ xq,
                                                         const uint16_t* __restrict__ xs,
                                                         const uint8_t* __restrict__ wq,
                                                         const uint16_t* __restrict__ ws,
@@ -106,15 +165,12 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const uint8_t* __restric
                         acc[r][m] = __builtin_fmaf((float)d, sxv * bf16_to_f32(cur.s[r][t]), acc[r][m]);
                     }
                 }
+#if WUSH_GEMV_TBAR
+                // keep one group's activations live at a time (M x 20 B per lane)
+                if constexpr (M > 1) __builtin_amdgcn_sched_barrier(0);
+#endif
             }
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const float v = wave_sum_dpp(acc[r][m]);
-                    if (lane == 0 && n0 + r < n_end) y[(size_t)m * N + n0 + r] = f32_to_f16_bits(v);
-                }
-            }
+            store_outputs<M, R>(acc, lane, n0, n_end, N, y);
             if (more) cur = nxt;
         }
     } else {
@@ -148,14 +204,7 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const uint8_t* __restric
                     }
                 }
             }
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const float v = wave_sum_dpp(acc[r][m]);
-                    if (lane == 0 && n0 + r < n_end) y[(size_t)m * N + n0 + r] = f32_to_f16_bits(v);
-                }
-            }
+            store_outputs<M, R>(acc, lane, n0, n_end, N, y);
         }
     }
 }
@@ -214,13 +263,13 @@ extern "C" int wush_gemv_int4(const uint8_t* xq, const uint16_t* xs, const uint8
     const int n = (int)N, k = (int)K;
     switch (M) {
         case 1: wush::launch_gemv<1, WUSH_GEMV_R1>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 2: wush::launch_gemv<2, 4>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 3: wush::launch_gemv<3, 2>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 4: wush::launch_gemv<4, 2>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 5: wush::launch_gemv<5, 1>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 6: wush::launch_gemv<6, 1>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 7: wush::launch_gemv<7, 1>(xq, xs, wq, ws, y, n, k, stream); break;
-        default: wush::launch_gemv<8, 1>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 2: wush::launch_gemv<2, WUSH_GEMV_R2>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 3: wush::launch_gemv<3, WUSH_GEMV_R4>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 4: wush::launch_gemv<4, WUSH_GEMV_R4>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 5: wush::launch_gemv<5, WUSH_GEMV_R8>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 6: wush::launch_gemv<6, WUSH_GEMV_R8>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 7: wush::launch_gemv<7, WUSH_GEMV_R8>(xq, xs, wq, ws, y, n, k, stream); break;
+        default: wush::launch_gemv<8, WUSH_GEMV_R8>(xq, xs, wq, ws, y, n, k, stream); break;
     }
     return (int)hipGetLastError();
 }

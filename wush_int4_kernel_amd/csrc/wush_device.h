@@ -105,6 +105,78 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// ---------------------------------------------------------------------------
+// Sum of V values (V a power of two, 1..64) over the 64 lanes of a wavefront
+// by recursive halving.  At each step a lane keeps half of its values and adds
+// its partner's copies of that half: partners across lane halves and 16-lane
+// rows are exchanged with v_permlane32_swap / v_permlane16_swap, within a row
+// with DPP (row_mirror, row_half_mirror, quad swaps).  Once one value is left,
+// the remaining steps are plain pair sums.  V outputs cost about 2V + 3 log V
+// VALU operations instead of ~8 per output with one full reduction each.
+// Every lane returns the total of value wave_rs_index<V>(lane); the lanes with
+// (lane & (64 / V - 1)) == 0 hold each index exactly once.
+// Summation order differs from a sequential sum (fp32, tolerance-checked).
+template <int D>
+__device__ __forceinline__ float dpp_partner(float v) {
+    constexpr int ctrl = D == 8 ? 0x140 : D == 4 ? 0x141 : D == 2 ? 0x4E : 0xB1;
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xf, 0xf, false));
+}
+
+// (a, b) -> the pair v_permlane{32,16}_swap leaves: a's lanes in the upper
+// half (odd rows) exchanged with b's lanes in the lower half (even rows).
+template <int D>
+__device__ __forceinline__ float lanes_swap_sum(float a, float b) {
+    if constexpr (D == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+}
+
+template <int D, int H, int V>
+__device__ __forceinline__ void rs_step(float (&v)[V], int lane) {
+    if constexpr (H == 0) {                       // one value left: pair sum
+        if constexpr (D >= 16) v[0] = lanes_swap_sum<D>(v[0], v[0]);
+        else v[0] = v[0] + dpp_partner<D>(v[0]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            if constexpr (D >= 16) {
+                // lanes with bit D clear keep i, the others i + H
+                v[i] = lanes_swap_sum<D>(v[i], v[i + H]);
+            } else {
+                const bool up = (lane & D) != 0;
+                const float keep = up ? v[i + H] : v[i];
+                const float send = up ? v[i] : v[i + H];
+                v[i] = keep + dpp_partner<D>(send);
+            }
+        }
+    }
+}
+
+template <int V>
+__device__ __forceinline__ float wave_reduce_scatter(float (&v)[V], int lane) {
+    static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V: power of two <= 64");
+    rs_step<32, V / 2>(v, lane);
+    rs_step<16, V / 4>(v, lane);
+    rs_step<8, V / 8>(v, lane);
+    rs_step<4, V / 16>(v, lane);
+    rs_step<2, V / 32>(v, lane);
+    rs_step<1, V / 64>(v, lane);
+    return v[0];
+}
+
+template <int V>
+__device__ __forceinline__ int wave_rs_index(int lane) {
+    int idx = 0;
+#pragma unroll
+    for (int j = 0; (1 << (j + 1)) <= V; ++j)
+        if (lane & (32 >> j)) idx += V >> (j + 1);
+    return idx;
+}
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte streaming load with the non-temporal hint (weights are read once).
