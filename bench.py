@@ -66,6 +66,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--K", type=int, default=K_L70)
     ap.add_argument("--N", type=int, default=N_L70)
+    ap.add_argument("--counter-workload", action="store_true",
+                    help="launch every kernel of the path 3 times, then a 512 MiB copy (rocprofv3 --pmc)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only launch the M=1 dominant kernel (for rocprofv3 runs)")
     return ap.parse_args()
@@ -187,6 +189,44 @@ def main():
         print(json.dumps({"kernel_only": "gemv_int4", "launches": args.warmup + args.steps,
                           "gemv_algorithmic_bytes": gemv_bytes(M, N, K),
                           "copy_bytes_each_way": src.numel() * 2}))
+        return
+
+    # ------------------------------------------------- hardware-counter workload
+    if args.counter_workload:
+        # Each kernel of the path three times on bench shapes, then the copy
+        # that calibrates FETCH_SIZE / WRITE_SIZE.  For rocprofv3 --pmc passes.
+        def launch_product(kind, M_, N_, K_, wq_, ws_, reps=3):
+            xq_, xs_ = _C.quant_int4(activations_k(M_, K_))
+            y_ = torch.empty(M_, N_, dtype=torch.float16, device=dev)
+            for _ in range(reps):
+                if kind == "gemv":
+                    capi.gemv_int4(xq_.data_ptr(), xs_.data_ptr(), wq_.data_ptr(), ws_.data_ptr(), y_.data_ptr(),
+                                   M_, N_, K_, stream.cuda_stream)
+                else:
+                    capi.gemm_s4(xq_.data_ptr(), xs_.data_ptr(), wq_.data_ptr(), ws_.data_ptr(), y_.data_ptr(),
+                                 M_, N_, K_, None, 0, stream.cuda_stream)
+
+        def activations_k(M_, K_):
+            return torch.randn(M_, K_, generator=gdev, device=dev).to(torch.bfloat16)
+
+        launch_product("gemv", 1, N, K, wq, ws)            # L70 M=1 decode
+        launch_product("gemv", 8, N, K, wq, ws)            # L70 M=8 decode
+        launch_product("gemm", 32, N, K, wq, ws)           # L70 M=32 (32x32 streaming GEMM)
+        for _ in range(3):
+            _C.fused_transform_quant_int4_smallm(activations(1, gdev).to(torch.bfloat16), T)
+            _C.fused_transform_quant_int4(activations(4096, gdev).to(torch.bfloat16), T)
+            _C.quant_int4(Wt)
+        Wq8, Ws8 = _C.quant_int4((torch.randn(24576, 4096, generator=gdev, device=dev) * 0.02).to(torch.bfloat16))
+        launch_product("gemm", 8, 24576, 4096, Wq8, Ws8)   # Qwen3-8B M=8 (16x16x64 streaming GEMM)
+        W3, S3 = _C.quant_int4((torch.randn(4096, 4096, generator=gdev, device=dev) * 0.02).to(torch.bfloat16))
+        launch_product("gemm", 4096, 4096, 4096, W3, S3)  # 4096^3 prefill tiles
+        torch.cuda.synchronize()
+        src = torch.empty(256 << 20, dtype=torch.int16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"counter_workload": "done", "copy_bytes_each_way": src.numel() * 2}))
         return
 
     # ------------------------------------------------------------- layer sweep

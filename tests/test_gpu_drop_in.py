@@ -207,7 +207,7 @@ def test_gemv_ops(C):
 @pytest.mark.parametrize("M", [1, 2, 5, 6, 7, 8])
 def test_decode_ops_route_to_either_kernel(C, M):
     # w4a4_gemm_s4 and w4a4_gemv_multi pick the dot8 GEMV or the MFMA GEMM by
-    # (M, N*K): small weights at M 7-8 take the GEMM, N*K >= 2^28 the GEMV.
+    # (M, N*K): small weights at M = 8 take the GEMM, N*K >= 2^28 the GEMV.
     # Either way the result is the same product (checked on sampled columns).
     import torch
     g = rng(60 + M)

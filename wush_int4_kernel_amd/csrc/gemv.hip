@@ -22,9 +22,13 @@ namespace wush {
 
 // Tuning knobs (defaults measured at K=8192 N=57344 and K=4096 N=24576).
 #ifndef WUSH_GEMV_WAVES
-#define WUSH_GEMV_WAVES 4       // wavefronts per workgroup (2 / 8 / 16 measured no better)
+#define WUSH_GEMV_WAVES 4       // wavefronts per workgroup at M = 1 (2 / 8 / 16 no better)
 #endif
-constexpr int kGemvWaves = WUSH_GEMV_WAVES;
+#ifndef WUSH_GEMV_WAVES_M
+#define WUSH_GEMV_WAVES_M 16    // ... for M >= 2: the staged activations (M*K*5/8 bytes of
+#endif                          // LDS) are shared by 16 wavefronts (L70 M=8: 51.5 vs 53.5 us)
+template <int M>
+constexpr int gemv_waves() { return M == 1 ? WUSH_GEMV_WAVES : WUSH_GEMV_WAVES_M; }
 #ifndef WUSH_GEMV_RS
 #define WUSH_GEMV_RS 1          // recursive-halving reduction of the R x M outputs
 #endif
@@ -103,7 +107,7 @@ __device__ __forceinline__ void store_outputs(const float (&acc)[R][M], int lane
 }
 
 template <int M, int R, int GPL>
-__global__ __launch_bounds__(64 * kGemvWaves) void gemv_int4_kernel(const uint8_t* __restrict__ xq,
+__global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const uint8_t* __restrict__ xq,
                                                         const uint16_t* __restrict__ xs,
                                                         const uint8_t* __restrict__ wq,
                                                         const uint16_t* __restrict__ ws,
@@ -117,7 +121,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_int4_kernel(const uint8_
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int n_begin = (blockIdx.x * kGemvWaves + wave) * rows_per_wave;
+    const int n_begin = (blockIdx.x * gemv_waves<M>() + wave) * rows_per_wave;
     const int n_end = min(N, n_begin + rows_per_wave);
 
     if constexpr (GPL > 0) {
@@ -217,6 +221,7 @@ static void launch_gemv_t(const uint8_t* xq, const uint16_t* xs, const uint8_t* 
     // Spread the rows evenly over the wavefronts that are resident at once
     // (occupancy from the kernel's register and LDS use), so every CU
     // finishes together.
+    constexpr int kGemvWaves = gemv_waves<M>();
     static int resident_waves = 0;
     if (resident_waves == 0) {
         int per_cu = 0;
