@@ -62,29 +62,38 @@ struct InputTraits<WUSH_DTYPE_F32> {
     }
 };
 
-// Codes of bf16 or fp16 inputs without a division per element.
-// Write sf = ms * 2^es (ms < 256, sf is a normal bf16) and v = mv * 2^ev
-// (|mv| < 2^11).  For a half-integer h, v/sf - h = (2v - 2h*sf) / (2 sf) and
-// the numerator is a multiple of 2^min(ev+1, es); if it is not zero and
-// |v/sf| is near h >= 0.5 (so 2^(ev-es) >= 0.5*128/2047), then
-// |v/sf - h| >= 2^(ev-es)/255 > 2^-13.  With r = RN(1/sf) and y = RN(v*r),
-// |y - v/sf| < 2^-20 for |v/sf| < 8.  Hence rint(y) == rint(RN(v/sf)) except
-// when v/sf is exactly a half-integer, and then |y - h| < 2^-20: such y
-// (within kHalfBand of a half-integer) are replaced by floor(y) + 0.5 = h
-// and rounded half to even like the reference.  |y| >= 8 clamps like
-// |v/sf| > 7.5; NaN and infinities give the codes of code_of.  Bit-identical
-// to code_of for bf16 and fp16 inputs; fp32 inputs keep the division.
-constexpr float kHalfBand = 0x1p-14f;
-__device__ __forceinline__ int code_of_narrow(float v, float r) {
+// Codes of a finite bf16 or fp16 group without a division per element:
+// clamp(rint(RN(v/sf)), -7, 7) from one reciprocal r = RN(1/sf) per group and
+// an fma correction per element.
+//  * y = RN(v*r) is within 2^-22 |v/sf| of the quotient.  v has at most 11
+//    significant bits and sf at most 8, so the remainder e = v - y*sf is a
+//    multiple of ulp(y)*ulp(sf) of about 9 bits: exactly representable, and
+//    fma computes it exactly.  y1 = RN(y + e*r) is the quotient up to 2^-46
+//    relative.
+//  * Write sf = ms*2^es (ms < 2^8) and v = mv*2^ev (|mv| < 2^11).  For a
+//    half-integer h, v/sf - h = (2v - 2h*sf) / (2sf) with a numerator that is
+//    a multiple of 2^min(ev+1, es); if it is not zero and v/sf is near
+//    h >= 0.5, |v/sf - h| >= 2^(ev-es)/255 > 2^-13.  So a quotient that is not
+//    a half-integer is far from every rounding tie and rint(y1) equals
+//    rint(RN(v/sf)); an exact half-integer quotient h comes out as y1 = h
+//    exactly (the perturbation is far below half an ulp of h).
+//  * Codes are formed as c + 8 in [1, 15]: adding 8 keeps the parity that
+//    round-half-even needs, and y1 + 8 cannot cross a half-integer.  They are
+//    converted straight into bytes with v_cvt_pk_u8_f32 and turned into two's
+//    complement nibbles by an xor with 8.
+// About 8 VALU operations per element, against about 15 with a tie band
+// around RN(v*r) and more with a division.  Checked against the division for
+// every finite bf16 and fp16 v (|v| < 1.8e19, i.e. s2 finite) and every bf16
+// sf >= 1e-8 (tests/test_quant_codes_exhaustive.py).  Groups with a non-finite
+// element (s2 not finite) take code_of, whose division handles inf and NaN.
+__device__ __forceinline__ float code_plus8(float v, float sf, float r) {
     const float y = v * r;
-    const float f = __builtin_floorf(y);
-    const float y2 = __builtin_fabsf(y - f - 0.5f) < kHalfBand ? f + 0.5f : y;
-    float c = __builtin_rintf(y2);
-    c = __builtin_fminf(__builtin_fmaxf(c, -7.0f), 7.0f);
-    return (y == y) ? (int)c : 0;
+    const float e = __builtin_fmaf(-y, sf, v);
+    const float y1 = __builtin_fmaf(e, r, y);
+    return __builtin_amdgcn_fmed3f(__builtin_rintf(y1 + 8.0f), 1.0f, 15.0f);
 }
 
-__device__ __forceinline__ uint32_t quant_group32_narrow(const float (&v)[32], uint32_t (&w)[4]) {
+__device__ __forceinline__ uint32_t quant_group32_fma(const float (&v)[32], uint32_t (&w)[4]) {
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
@@ -93,15 +102,83 @@ __device__ __forceinline__ uint32_t quant_group32_narrow(const float (&v)[32], u
     }
     float sf;
     const uint32_t sb = group_scale(s1, s2, &sf);
+    if (!__builtin_isfinite(s2)) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            uint32_t acc = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc |= (uint32_t)(code_of(v[d * 8 + e], sf) & 0xF) << (4 * e);
+            w[d] = acc;
+        }
+        return sb;
+    }
     const float r = 1.0f / sf;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-        uint32_t acc = 0;
+        // even elements 8d+2k -> byte k of a, odd elements 8d+2k+1 -> byte k of b
+        uint32_t a = 0, b = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc |= (uint32_t)(code_of_narrow(v[d * 8 + e], r) & 0xF) << (4 * e);
-        w[d] = acc;
+        for (int k = 0; k < 4; ++k) {
+            a = __builtin_amdgcn_cvt_pk_u8_f32(code_plus8(v[8 * d + 2 * k], sf, r), k, a);
+            b = __builtin_amdgcn_cvt_pk_u8_f32(code_plus8(v[8 * d + 2 * k + 1], sf, r), k, b);
+        }
+        w[d] = (a ^ 0x08080808u) | ((b ^ 0x08080808u) << 4);
     }
     return sb;
+}
+
+// 2-byte inputs: the wavefront's 64 groups (4 KiB) are read with four
+// load instructions of 1 KiB contiguous each, then redistributed so that
+// lane l holds group l.  Instruction c gives lane l the 16 bytes at
+// c*1024 + 16*sig(l), sig(l) = 4*(l%16) + l/16: quarter l/16 of group
+// 16c + l%16.  A 4x4 transpose between register index c and lane bits 5..4
+// (v_permlane32_swap on register pairs (c, c+2), then v_permlane16_swap on
+// (c, c+1)) leaves quarter p of group l in register p of lane l.  All lanes
+// take part; lanes past the last group load zeros and store nothing.
+__device__ __forceinline__ void swap_regs32(uint4& a, uint4& b) {
+    auto x = __builtin_amdgcn_permlane32_swap(a.x, b.x, false, false);
+    auto y = __builtin_amdgcn_permlane32_swap(a.y, b.y, false, false);
+    auto z = __builtin_amdgcn_permlane32_swap(a.z, b.z, false, false);
+    auto w = __builtin_amdgcn_permlane32_swap(a.w, b.w, false, false);
+    a = make_uint4(x[0], y[0], z[0], w[0]);
+    b = make_uint4(x[1], y[1], z[1], w[1]);
+}
+__device__ __forceinline__ void swap_regs16(uint4& a, uint4& b) {
+    auto x = __builtin_amdgcn_permlane16_swap(a.x, b.x, false, false);
+    auto y = __builtin_amdgcn_permlane16_swap(a.y, b.y, false, false);
+    auto z = __builtin_amdgcn_permlane16_swap(a.z, b.z, false, false);
+    auto w = __builtin_amdgcn_permlane16_swap(a.w, b.w, false, false);
+    a = make_uint4(x[0], y[0], z[0], w[0]);
+    b = make_uint4(x[1], y[1], z[1], w[1]);
+}
+
+template <int DT>
+__device__ __forceinline__ void load_group_coalesced(const void* x, int64_t g, int64_t n_groups, float (&v)[32]) {
+    const int lane = threadIdx.x & 63;
+    const int64_t g0 = g - lane;                     // first group of the wavefront
+    const int sig = 4 * (lane & 15) + (lane >> 4);
+    const uint16_t* base = static_cast<const uint16_t*>(x);
+    uint4 r[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int64_t gi = g0 + 16 * c + (sig >> 2);
+        r[c] = gi < n_groups ? load_nt16(base + gi * 32 + (sig & 3) * 8) : make_uint4(0, 0, 0, 0);
+    }
+    swap_regs32(r[0], r[2]);
+    swap_regs32(r[1], r[3]);
+    swap_regs16(r[0], r[1]);
+    swap_regs16(r[2], r[3]);
+    const uint32_t* u = reinterpret_cast<const uint32_t*>(r);
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+        if constexpr (DT == WUSH_DTYPE_BF16) {
+            v[2 * d] = bf16_to_f32(u[d] & 0xffffu);
+            v[2 * d + 1] = __uint_as_float(u[d] & 0xffff0000u);
+        } else {
+            v[2 * d] = f16_to_f32(u[d] & 0xffffu);
+            v[2 * d + 1] = f16_to_f32(u[d] >> 16);
+        }
+    }
 }
 
 template <int DT>
@@ -110,11 +187,16 @@ __global__ __launch_bounds__(256) void quant_int4_kernel(const void* __restrict_
                                                          uint16_t* __restrict__ s,
                                                          int64_t n_groups) {
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= n_groups) return;
     float v[32];
-    InputTraits<DT>::load(x, g, v);
+    if constexpr (DT == WUSH_DTYPE_F32) {
+        if (g >= n_groups) return;
+        InputTraits<DT>::load(x, g, v);
+    } else {
+        load_group_coalesced<DT>(x, g, n_groups, v);   // whole wavefront, before any exit
+        if (g >= n_groups) return;
+    }
     uint32_t w[4];
-    const uint32_t sb = DT == WUSH_DTYPE_F32 ? quant_group32(v, w) : quant_group32_narrow(v, w);
+    const uint32_t sb = DT == WUSH_DTYPE_F32 ? quant_group32(v, w) : quant_group32_fma(v, w);
     reinterpret_cast<uint4*>(q)[g] = make_uint4(w[0], w[1], w[2], w[3]);
     s[g] = (uint16_t)sb;
 }
