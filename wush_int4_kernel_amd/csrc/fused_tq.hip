@@ -9,10 +9,14 @@
 // fused_tq_device.h):
 //  * rows kernel (rows >= 384): lane = row, wavefront = 64 rows of one block c.
 //    T[c] is wave-uniform, so it is read with scalar loads into SGPRs and
-//    every product is v_mul with an SGPR operand: no LDS and no cross-lane
-//    traffic in the 2048-op inner loop.  4 wavefronts of a workgroup take 4
-//    adjacent blocks of the same 64 rows, so each row's 256 B of bf16 input
-//    is consumed by one workgroup.
+//    every MAC takes an SGPR operand: no LDS and no cross-lane traffic in the
+//    inner loop.  A product of two bf16 values is exact in fp32 unless an
+//    operand is extreme (tiny, huge, inf or NaN), and then fma(x, T, acc)
+//    equals the reference's acc + x*T bit for bit: when the wavefront's x and
+//    the block's T are all in range (checked per launch, almost always) the
+//    loop is 1024 v_fma_f32 per lane instead of 1024 v_mul + 1024 v_add.
+//    4 wavefronts of a workgroup take 4 adjacent blocks of the same 64 rows,
+//    so each row's 256 B of bf16 input is consumed by one workgroup.
 //  * small-M kernel (rows < 384: decode, small batches): 32 lanes per (row, block), two
 //    pairs per one-wavefront workgroup so a decode row spreads over K/64 CUs;
 //    lane j
@@ -41,8 +45,19 @@ __global__ __launch_bounds__(256) void fused_tq_rows_kernel(const uint16_t* __re
     const bool active = r < rows;
 
     float xv[32];
+    BfRange xr;
     if (active) {
-        load_bf16x32(x + r * K + c * 32, xv);
+        const uint4* p4 = reinterpret_cast<const uint4*>(x + r * K + c * 32);
+        uint4 raw[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) raw[k] = p4[k];
+        const uint32_t* u = reinterpret_cast<const uint32_t*>(raw);
+#pragma unroll
+        for (int d = 0; d < 16; ++d) {
+            xv[2 * d] = bf16_to_f32(u[d] & 0xffffu);
+            xv[2 * d + 1] = __uint_as_float(u[d] & 0xffff0000u);
+            xr.add(u[d]);
+        }
     } else {
 #pragma unroll
         for (int i = 0; i < 32; ++i) xv[i] = 0.0f;
@@ -50,17 +65,43 @@ __global__ __launch_bounds__(256) void fused_tq_rows_kernel(const uint16_t* __re
 
     // T[c][j][i] as bf16 pairs (i even in the low half), wave-uniform.
     const uint32_t* tc = reinterpret_cast<const uint32_t*>(t + c * 1024);
+    // Each lane checks 16 of the block's 1024 entries.
+    BfRange tr;
+    {
+        const uint4* t4 = reinterpret_cast<const uint4*>(tc) + lane * 2;
+        const uint4 a = t4[0], b = t4[1];
+        tr.add(a.x); tr.add(a.y); tr.add(a.z); tr.add(a.w);
+        tr.add(b.x); tr.add(b.y); tr.add(b.z); tr.add(b.w);
+    }
+    // x_i * T[c][j][i] of two bf16 values is exact in fp32 when both lie in
+    // the safe range, and then fma(x, T, acc) == acc + x*T bit for bit: one
+    // fma per MAC instead of a mul and an add.  Otherwise the sequential
+    // mul-then-add form, which also carries inf / NaN / underflow exactly.
     float xp[32];
+    if (__all(xr.safe() & tr.safe())) {
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        float acc = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            float acc = 0.0f;
 #pragma unroll
-        for (int d = 0; d < 16; ++d) {
-            const uint32_t pair = tc[j * 16 + d];
-            acc = acc + xv[2 * d] * bf16_to_f32(pair & 0xffffu);
-            acc = acc + xv[2 * d + 1] * __uint_as_float(pair & 0xffff0000u);
+            for (int d = 0; d < 16; ++d) {
+                const uint32_t pair = tc[j * 16 + d];
+                acc = __builtin_fmaf(xv[2 * d], bf16_to_f32(pair & 0xffffu), acc);
+                acc = __builtin_fmaf(xv[2 * d + 1], __uint_as_float(pair & 0xffff0000u), acc);
+            }
+            xp[j] = acc;
         }
-        xp[j] = acc;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 16; ++d) {
+                const uint32_t pair = tc[j * 16 + d];
+                acc = acc + xv[2 * d] * bf16_to_f32(pair & 0xffffu);
+                acc = acc + xv[2 * d + 1] * __uint_as_float(pair & 0xffff0000u);
+            }
+            xp[j] = acc;
+        }
     }
 
     uint32_t w[4];

@@ -12,6 +12,31 @@
 
 namespace wush {
 
+// Range check for exact bf16 x bf16 products, on packed pairs of bf16 bits.
+// A value is "safe" when it is zero or its magnitude bits m = bits & 0x7fff
+// lie in [0x1e00, 0x58ff], i.e. |v| in [2^-67, 2^51).  The product of two
+// safe values has at most 16 significant bits, its lowest bit is at least
+// 2^-148 and it is below 2^102, so it is exact in fp32 (no rounding,
+// underflow or overflow), and a sum of 32 of them stays finite.
+// BfRange accumulates, two values per 32-bit word, the largest m and the
+// smallest m - 1 (16-bit wrap-around sends zeros to 0xffff, out of the way)
+// with packed 16-bit integer min / max.
+struct BfRange {
+    uint32_t mx = 0u, mn = 0xffffffffu;
+    __device__ __forceinline__ void add(uint32_t w) {
+        typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+        const u16x2 m = __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
+        const u16x2 m1 = m - (u16x2){1, 1};
+        mx = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx), m));
+        mn = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, mn), m1));
+    }
+    __device__ __forceinline__ bool safe() const {
+        const uint32_t mx_lo = mx & 0xffffu, mx_hi = mx >> 16;
+        const uint32_t mn_lo = mn & 0xffffu, mn_hi = mn >> 16;
+        return (mx_lo <= 0x58ffu) & (mx_hi <= 0x58ffu) & (mn_lo >= 0x1dffu) & (mn_hi >= 0x1dffu);
+    }
+};
+
 __device__ __forceinline__ void load_bf16x32(const uint16_t* p, float (&v)[32]) {
     const uint4* p4 = reinterpret_cast<const uint4*>(p);
     uint4 r[4];

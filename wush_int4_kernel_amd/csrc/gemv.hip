@@ -32,6 +32,12 @@ constexpr int gemv_waves() { return M == 1 ? WUSH_GEMV_WAVES : WUSH_GEMV_WAVES_M
 #ifndef WUSH_GEMV_RS
 #define WUSH_GEMV_RS 1          // recursive-halving reduction of the R x M outputs
 #endif
+#ifndef WUSH_GEMV_MAXWAVES
+#define WUSH_GEMV_MAXWAVES 0
+#endif
+#ifndef WUSH_GEMV_INTERLEAVE
+#define WUSH_GEMV_INTERLEAVE 0
+#endif
 #ifndef WUSH_GEMV_TBAR
 #define WUSH_GEMV_TBAR 1        // scheduling barrier after each group (fewer live VGPRs)
 #endif
@@ -121,8 +127,17 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
+#if WUSH_GEMV_INTERLEAVE
+    // chunks of R rows dealt round-robin over the grid's wavefronts
+    (void)rows_per_wave;
+    const int n_begin = (blockIdx.x * gemv_waves<M>() + wave) * R;
+    const int n_step = gridDim.x * gemv_waves<M>() * R;
+    const int n_end = N;
+#else
     const int n_begin = (blockIdx.x * gemv_waves<M>() + wave) * rows_per_wave;
+    const int n_step = R;
     const int n_end = min(N, n_begin + rows_per_wave);
+#endif
 
     if constexpr (GPL > 0) {
         using Chunk = GemvChunk<R, GPL>;
@@ -147,9 +162,9 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
         for (int i = threadIdx.x; i < M * G; i += blockDim.x) xs_l[i] = bf16_to_f32(xs[i]);
         __syncthreads();
 
-        for (int n0 = n_begin; n0 < n_end; n0 += R) {
-            const bool more = n0 + R < n_end;
-            if (more) load(n0 + R, nxt);
+        for (int n0 = n_begin; n0 < n_end; n0 += n_step) {
+            const bool more = n0 + n_step < n_end;
+            if (more) load(n0 + n_step, nxt);
             __builtin_amdgcn_sched_barrier(0);
             float acc[R][M];
 #pragma unroll
@@ -182,7 +197,7 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
         for (int i = threadIdx.x; i < M * G; i += blockDim.x) xq_l[i] = xq4[i];
         for (int i = threadIdx.x; i < M * G; i += blockDim.x) xs_l[i] = bf16_to_f32(xs[i]);
         __syncthreads();
-        for (int n0 = n_begin; n0 < n_end; n0 += R) {
+        for (int n0 = n_begin; n0 < n_end; n0 += n_step) {
             float acc[R][M];
 #pragma unroll
             for (int r = 0; r < R; ++r)
@@ -233,9 +248,16 @@ static void launch_gemv_t(const uint8_t* xq, const uint16_t* xs, const uint8_t* 
             per_cu = 2;
         resident_waves = per_cu * kGemvWaves * cus;
     }
+#if WUSH_GEMV_INTERLEAVE
+    const int chunks = (N + R - 1) / R;
+    const int waves = min(WUSH_GEMV_MAXWAVES > 0 ? min(resident_waves, WUSH_GEMV_MAXWAVES) : resident_waves, chunks);
+    const int rows_per_wave = 0;
+    const int blocks = (waves + kGemvWaves - 1) / kGemvWaves;
+#else
     int rows_per_wave = (N + resident_waves - 1) / resident_waves;
     rows_per_wave = max(rows_per_wave, 1);
     const int blocks = (N + kGemvWaves * rows_per_wave - 1) / (kGemvWaves * rows_per_wave);
+#endif
     gemv_int4_kernel<M, R, GPL><<<dim3(blocks), dim3(64 * kGemvWaves), smem, stream>>>(xq, xs, wq, ws, y, N, K,
                                                                                         rows_per_wave);
 }
