@@ -175,6 +175,32 @@ def test_fused_random(capi, rows, K):
     assert np.array_equal(s, so)
 
 
+@pytest.mark.parametrize("rows", [5, 448])
+def test_fused_extreme_operands_both_loops(capi, rows):
+    # The rows kernel (rows >= 384) runs an fma loop when every nonzero |x| of
+    # a wavefront's rows and |T| of its block lies in [2^-67, 2^51), and the
+    # mul-then-add loop otherwise.  Plant out-of-range values in some rows and
+    # T blocks (tiny, subnormal, huge, inf, NaN, at the range edges) so both
+    # loops and the vote between them run; every code and scale must still
+    # match the oracle bit for bit.
+    g = rng(2003 + rows)
+    K = 256
+    xb = outlier_activations(g, rows, K)
+    tb = f32_to_bf16_bits(g.standard_normal((K // 32, 32, 32)) * 0.25)
+    specials = [0x0001, 0x8001, 0x0080, 0x1DFF, 0x1E00, 0x58FF, 0x5900, 0x7F7F, 0x7F80, 0xFF80, 0x7FC0,
+                0x2000, 0x0C00, 0x6000]
+    for r in range(0, rows, 7):
+        xb[r, g.integers(0, K)] = specials[r % len(specials)]
+    tb[1, 3, 5] = 0x0001            # subnormal T entry: block 1 takes mul + add
+    tb[2, 0, 0] = 0x1DFF            # just below the range
+    tb[3, 7, 9] = 0x58FF            # upper edge, still in range
+    tb[4, 1, 1] = 0x5900            # just above the range
+    q, s = run_fused(capi, xb, tb)
+    qo, so = oracle.fused_tq(xb, tb)
+    assert np.array_equal(q, qo), np.argwhere(q != qo)[:5]
+    assert np.array_equal(s, so), np.argwhere(s != so)[:5]
+
+
 def test_fused_permutation_identity_zeros(capi):
     g = rng(2001)
     K = 128
