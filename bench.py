@@ -284,7 +284,7 @@ def main():
     t = time_graph(g2, reps, args.steps, args.warmup)
     del g2
     tq_bytes = 2 * Mc * Kc + 64 * Kc + Mc * Kc // 2 + Mc * Kc // 16
-    tq_lane_ops = 64 * Mc * Kc          # one mul and one add per MAC, 32 MACs per element
+    tq_lane_ops = 32 * Mc * Kc          # one exact-product fma per MAC, 32 MACs per element
     ops["fused_tq_cfg2"] = {
         "us": round(t * 1e6, 2), "shape": f"X {Mc}x{Kc} bf16, T {Kc // 32}x32x32",
         "hbm_bytes": tq_bytes, "hbm_gbs": round(tq_bytes / t / 1e9, 1),

@@ -206,12 +206,13 @@ def test_gemv_ops(C):
 
 @pytest.mark.parametrize("M", [1, 2, 5, 6, 7, 8])
 def test_decode_ops_route_to_either_kernel(C, M):
-    # w4a4_gemm_s4 and w4a4_gemv_multi pick the dot8 GEMV or the MFMA GEMM by
-    # (M, N*K): small weights at M = 8 take the GEMM, N*K >= 2^28 the GEMV.
-    # Either way the result is the same product (checked on sampled columns).
+    # w4a4_gemm_s4 and w4a4_gemv_multi run the dot8 GEMV when its LDS staging
+    # (M*K*3/4 bytes) fits in 64 KiB and the MFMA GEMM otherwise (K = 16384 at
+    # M >= 6).  Either way the two ops give the same product (checked on
+    # sampled columns against the oracle).
     import torch
     g = rng(60 + M)
-    for N, K in [(4096, 4096), (32768, 8192)]:
+    for N, K in [(4096, 4096), (32768, 8192), (1024, 16384)]:
         wq, ws = C.quant_int4(to_dev_bf16(_bf16(g, (N, K), 0.02)))
         xq, xs = C.quant_int4(to_dev_bf16(_bf16(g, (M, K))))
         cols = torch.from_numpy(np.sort(g.choice(N, size=512, replace=False))).cuda()

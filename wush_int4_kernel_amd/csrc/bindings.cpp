@@ -104,16 +104,16 @@ void check_packed(const torch::Tensor& xq, const torch::Tensor& xs, const torch:
 }
 
 // Which kernel family computes a product with M activation rows.  Both give
-// the same math (exact int32 group dots folded in fp32).  Measured on MI355X:
+// the same math (exact int32 group dots folded in fp32).  Measured on MI355X,
 // the dot8 streaming GEMV (wush_gemv_int4) is faster than the int8-MFMA
-// streaming GEMM (wush_gemm_s4) up to M = 7 at every shape measured (Llama-70B
-// FFN K=8192 N=57344 M=4: 42.4 vs 54.9 us; Qwen3-8B K=4096 N=24576 M=7: 14.2
-// vs 14.9 us) and at M = 8 once the weights are large (N*K >= 2^28;
-// Llama-70B M=8: 51.5 vs 56.5 us, Qwen3-8B M=8: 15.1 vs 15.0 us).  The GEMV
-// stages M*K*(1/2 + 1/8) bytes of activations in LDS, at most 64 KiB.
+// streaming GEMM (wush_gemm_s4) at every M <= 8 measured (Llama-70B FFN
+// K=8192 N=57344 M=8: 51.1 vs 56.5 us; Qwen3-8B K=4096 N=24576 M=8: 13.9 vs
+// 15.0 us).  The GEMV stages M*K*(1/2 + 1/4) bytes of activation codes and
+// scale terms in LDS, at most 64 KiB; larger M*K take the GEMM.
 bool gemv_preferred(int64_t M, int64_t N, int64_t K) {
-    const bool lds_fits = M * (K / 2) + M * (K / 32) * 4 <= 64 * 1024;
-    return lds_fits && M >= 1 && (M <= 7 || (M <= 8 && N * K >= (int64_t(1) << 28)));
+    (void)N;
+    const bool lds_fits = M * (K / 2) + M * (K / 32) * 8 <= 64 * 1024;
+    return lds_fits && M >= 1 && M <= 8;
 }
 
 // Shared product launch: y (M, N) fp16 = group-scaled product.

@@ -9,7 +9,9 @@
 // instruction of a wavefront reads 1 KiB of contiguous codes (16 B per lane)
 // and 128 B of contiguous scales.  The group dot is 4 v_dot8_i32_i4 on the
 // packed nibbles as stored (element 2k low nibble pairs with element 2k low
-// nibble), the fold is one cvt + one mul + one fma in fp32.  A chunk of R
+// nibble).  The fold is one cvt + one mul + one fma in fp32 at M = 1; for
+// M >= 2 the dot starts from the bits of 1.5*2^23, so two fmas fold it
+// without a conversion (see kMagicBits).  A chunk of R
 // weight rows (R = 1 at M = 1, else 2) is reduced over the wavefront at once:
 // the R x M partial sums go through a recursive-halving reduction (permlane
 // swaps and DPP, VALU only) that costs about two operations per output.  The
@@ -54,8 +56,8 @@ constexpr int gemv_waves() { return M == 1 ? WUSH_GEMV_WAVES : WUSH_GEMV_WAVES_M
 #define WUSH_GEMV_R8 2          // ... at M = 5 .. 8
 #endif
 
-__device__ __forceinline__ int dot32_s4(const uint4& a, const uint4& b) {
-    int d = __builtin_amdgcn_sdot8((int)a.x, (int)b.x, 0, false);
+__device__ __forceinline__ int dot32_s4(const uint4& a, const uint4& b, int init = 0) {
+    int d = __builtin_amdgcn_sdot8((int)a.x, (int)b.x, init, false);
     d = __builtin_amdgcn_sdot8((int)a.y, (int)b.y, d, false);
     d = __builtin_amdgcn_sdot8((int)a.z, (int)b.z, d, false);
     d = __builtin_amdgcn_sdot8((int)a.w, (int)b.w, d, false);
@@ -112,6 +114,46 @@ __device__ __forceinline__ void store_outputs(const float (&acc)[R][M], int lane
     }
 }
 
+// Fold without an int -> float conversion (M >= 2): the dot products start
+// from kMagicBits, the bits of kMagic = 1.5 * 2^23, so the int32 result read
+// as a float is kMagic + dot exactly (|dot| <= 1568).
+constexpr int kMagicBits = 0x4B400000;
+constexpr float kMagic = 12582912.0f;
+
+// Activation scales for which the conversion-free fold is exact: finite and
+// |sx| <= 2^60, so -kMagic*sx is exact and finite.
+__device__ __forceinline__ bool scale_in_range(float s) { return __builtin_fabsf(s) <= 0x1p60f; }
+
+// Activation scales in LDS: sx at M = 1 (plain fold), (sx, -kMagic*sx) for
+// M >= 2.
+template <int M> struct XsStageT { using type = float2; };
+template <> struct XsStageT<1> { using type = float; };
+template <int M> using XsStage = typename XsStageT<M>::type;
+__device__ __forceinline__ float xs_at(const float* xs_l, int i) { return xs_l[i]; }
+__device__ __forceinline__ float xs_at(const float2* xs_l, int i) { return xs_l[i].x; }
+
+// Stage the activation codes and scales in LDS; for M >= 2 returns whether
+// every sx of the block is in range (block-uniform).
+template <int M>
+__device__ __forceinline__ bool stage_activations(const uint8_t* __restrict__ xq, const uint16_t* __restrict__ xs,
+                                                  uint4* xq_l, XsStage<M>* xs_l, int G) {
+    const uint4* xq4 = reinterpret_cast<const uint4*>(xq);
+    for (int i = threadIdx.x; i < M * G; i += blockDim.x) xq_l[i] = xq4[i];
+    if constexpr (M == 1) {
+        for (int i = threadIdx.x; i < G; i += blockDim.x) xs_l[i] = bf16_to_f32(xs[i]);
+        __syncthreads();
+        return false;
+    } else {
+        int bad = 0;
+        for (int i = threadIdx.x; i < M * G; i += blockDim.x) {
+            const float sx = bf16_to_f32(xs[i]);
+            xs_l[i] = make_float2(sx, -kMagic * sx);
+            bad |= !scale_in_range(sx);
+        }
+        return !__syncthreads_or(bad);
+    }
+}
+
 template <int M, int R, int GPL>
 __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const uint8_t* __restrict__ xq,
                                                         const uint16_t* __restrict__ xs,
@@ -122,8 +164,9 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
     extern __shared__ __align__(16) uint8_t smem[];
     const int G = K >> 5;
     const int K2 = K >> 1;
-    uint4* xq_l = reinterpret_cast<uint4*>(smem);                 // [M][G] x 16 B
-    float* xs_l = reinterpret_cast<float*>(smem + (size_t)M * K2); // [M][G]
+    using XS = XsStage<M>;
+    uint4* xq_l = reinterpret_cast<uint4*>(smem);                       // [M][G] x 16 B
+    XS* xs_l = reinterpret_cast<XS*>(smem + (size_t)M * K2);            // [M][G]
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -157,10 +200,7 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
         Chunk cur, nxt;
         if (n_begin < n_end) load(n_begin, cur);
 
-        const uint4* xq4 = reinterpret_cast<const uint4*>(xq);
-        for (int i = threadIdx.x; i < M * G; i += blockDim.x) xq_l[i] = xq4[i];
-        for (int i = threadIdx.x; i < M * G; i += blockDim.x) xs_l[i] = bf16_to_f32(xs[i]);
-        __syncthreads();
+        const bool x_in_range = stage_activations<M>(xq, xs, xq_l, xs_l, G);
 
         for (int n0 = n_begin; n0 < n_end; n0 += n_step) {
             const bool more = n0 + n_step < n_end;
@@ -171,32 +211,58 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
             for (int r = 0; r < R; ++r)
 #pragma unroll
                 for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
+            if (M > 1 && x_in_range) {
+                if constexpr (M > 1) {
+                // d' = kMagicBits + dot, read as a float, is kMagic + dot
+                // exactly, so fma(d', sx, -kMagic*sx) = dot*sx exactly (at most
+                // 19 significant bits) without a conversion, and fma(dot*sx, sw,
+                // acc) rounds dot*sx*sw + acc once, like fma(dot, sx*sw, acc)
+                // with its exact bf16 x bf16 factor: one VALU operation fewer
+                // per output.
 #pragma unroll
-            for (int t = 0; t < GPL; ++t) {
-                const int g = lane + 64 * t;
+                for (int t = 0; t < GPL; ++t) {
+                    const int g = lane + 64 * t;
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const uint4 xv = xq_l[m * G + g];
-                    const float sxv = xs_l[m * G + g];
+                    for (int m = 0; m < M; ++m) {
+                        const uint4 xv = xq_l[m * G + g];
+                        const float2 sx2 = xs_l[m * G + g];
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        const int d = dot32_s4(cur.w[r][t], xv);
-                        acc[r][m] = __builtin_fmaf((float)d, sxv * bf16_to_f32(cur.s[r][t]), acc[r][m]);
+                        for (int r = 0; r < R; ++r) {
+                            const int d = dot32_s4(cur.w[r][t], xv, kMagicBits);
+                            const float v = __builtin_fmaf(__int_as_float(d), sx2.x, sx2.y);
+                            acc[r][m] = __builtin_fmaf(v, bf16_to_f32(cur.s[r][t]), acc[r][m]);
+                        }
                     }
-                }
 #if WUSH_GEMV_TBAR
-                // keep one group's activations live at a time (M x 20 B per lane)
-                if constexpr (M > 1) __builtin_amdgcn_sched_barrier(0);
+                    // keep one group's activations live at a time (M x 24 B per lane)
+                    __builtin_amdgcn_sched_barrier(0);
 #endif
+                }
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < GPL; ++t) {
+                    const int g = lane + 64 * t;
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const uint4 xv = xq_l[m * G + g];
+                        const float sxv = xs_at(xs_l, m * G + g);
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            const int d = dot32_s4(cur.w[r][t], xv);
+                            acc[r][m] = __builtin_fmaf((float)d, sxv * bf16_to_f32(cur.s[r][t]), acc[r][m]);
+                        }
+                    }
+#if WUSH_GEMV_TBAR
+                    if constexpr (M > 1) __builtin_amdgcn_sched_barrier(0);
+#endif
+                }
             }
             store_outputs<M, R>(acc, lane, n0, n_end, N, y);
             if (more) cur = nxt;
         }
     } else {
-        const uint4* xq4 = reinterpret_cast<const uint4*>(xq);
-        for (int i = threadIdx.x; i < M * G; i += blockDim.x) xq_l[i] = xq4[i];
-        for (int i = threadIdx.x; i < M * G; i += blockDim.x) xs_l[i] = bf16_to_f32(xs[i]);
-        __syncthreads();
+        (void)stage_activations<M>(xq, xs, xq_l, xs_l, G);
         for (int n0 = n_begin; n0 < n_end; n0 += n_step) {
             float acc[R][M];
 #pragma unroll
@@ -215,7 +281,7 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     const uint4 xv = xq_l[m * G + g];
-                    const float sxv = xs_l[m * G + g];
+                    const float sxv = xs_at(xs_l, m * G + g);
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
                         const int d = dot32_s4(wv[r], xv);
@@ -232,7 +298,7 @@ template <int M, int R, int GPL>
 static void launch_gemv_t(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                           uint16_t* y, int N, int K, hipStream_t stream) {
     const int G = K / 32;
-    const size_t smem = (size_t)M * (K / 2) + (size_t)M * G * sizeof(float);
+    const size_t smem = (size_t)M * (K / 2) + (size_t)M * G * sizeof(XsStage<M>);
     // Spread the rows evenly over the wavefronts that are resident at once
     // (occupancy from the kernel's register and LDS use), so every CU
     // finishes together.
@@ -285,8 +351,8 @@ extern "C" int wush_gemv_int4(const uint8_t* xq, const uint16_t* xs, const uint8
     WUSH_REQUIRE(xq && xs && wq && ws && y);
     WUSH_REQUIRE(((uintptr_t)xq & 15u) == 0 && ((uintptr_t)wq & 15u) == 0);
     WUSH_REQUIRE(((uintptr_t)xs & 1u) == 0 && ((uintptr_t)ws & 1u) == 0 && ((uintptr_t)y & 1u) == 0);
-    // LDS holds M*K/2 code bytes + M*K/32 fp32 scales: 160 KiB per CU bounds K.
-    WUSH_REQUIRE((size_t)M * (K / 2) + (size_t)M * (K / 32) * 4 <= 64 * 1024);
+    // LDS holds M*K/2 code bytes + M*K/32 pairs of fp32 scale terms.
+    WUSH_REQUIRE((size_t)M * (K / 2) + (size_t)M * (K / 32) * 8 <= 64 * 1024);
     const int n = (int)N, k = (int)K;
     switch (M) {
         case 1: wush::launch_gemv<1, WUSH_GEMV_R1>(xq, xs, wq, ws, y, n, k, stream); break;
