@@ -59,7 +59,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--ms", default="1,8,32,4096", help="comma-separated M values")
+    ap.add_argument("--ms", default="1,8,32,64,4096", help="comma-separated M values")
     ap.add_argument("--copies", type=int, default=3, help="distinct weight copies (MALL defeat)")
     ap.add_argument("--graph-steps", type=int, default=12, help="layer steps captured in one HIP graph")
     ap.add_argument("--no-blas", action="store_true", help="skip the hipBLASLt bf16 baseline")

@@ -1,7 +1,7 @@
 """The reference's own tests, restated against the drop-in ``my_int4._C``.
 
 Each test follows a reference test script (tests/test_s2.py, test_sw2.py,
-test_s3.py, test_p13.py, test_p12.py, test_sw3.py of the reference) with the
+test_s3.py, test_p13.py, test_p12.py, test_sw3.py, test_final.py of the reference) with the
 same inputs, shapes and gates; the truth values come from the CPU oracle
 (the reference's rtn_int4 / ref_fused semantics) instead of the torch
 reference, and inputs are drawn on the CPU (a GPU RNG stream would not
@@ -148,6 +148,41 @@ def test_p13_outlier_e2e_gate(C):
     y = C.w4a4_gemm_s4(xqw, xsw, wqw, wsw).double().cpu()
     e = ((y - Yt).norm() / Yt.norm()).item()
     assert e <= 0.082, e
+
+
+def test_sw3_wmma_chain_and_final_gate(C):
+    # reference tests/test_sw3.py:11-38 and tests/test_final.py:61-77: the WMMA
+    # fused entry point against v0 (code flips < 2%, scales within 1e-2; here
+    # the same bit-exact kernel serves both, so no code flips at all), and the
+    # WMMA chain with w4a4_gemm_v1 (T rounded to bf16 on both sides) and with
+    # w4a4_gemm_v2 (weights transformed by the fp64 T) under 10% relative
+    # Frobenius error against X W^T in fp64.
+    import torch
+    from wush_int4_kernel_amd.wush_transform import compute_wush_transform, transform_weights
+    g = rng(7)
+    M, N, K, GT = 2048, 512, 4096, 32
+    X = bf16_bits_to_f32(_bf16(g, (M, K)))
+    W = bf16_bits_to_f32(_bf16(g, (N, K)))
+    X[:, 5::GT] *= 15.0
+    W[:, 12::GT] *= 8.0
+    Xb, Wb = f32_to_bf16_bits(X), f32_to_bf16_bits(W)
+    Xd = torch.from_numpy(bf16_bits_to_f32(Xb)).double()
+    Wd = torch.from_numpy(bf16_bits_to_f32(Wb)).double()
+    Xc = g.standard_normal((256, K)).astype(np.float32)
+    Xc[:, 5::GT] *= 15.0
+    T64 = compute_wush_transform(torch.from_numpy(Xc).double(), Wd)
+    Tb = T64.to(torch.bfloat16).cuda().contiguous()
+    Xg = to_dev_bf16(Xb)
+    q0, s0 = C.fused_transform_quant_int4(Xg, Tb)
+    q1, s1 = C.fused_transform_quant_int4_wmma(Xg, Tb)
+    assert torch.equal(q0, q1) and torch.equal(s0, s1)
+    Yt = Xd @ Wd.T
+    for w_t, gemm in ((Tb.double().cpu(), "w4a4_gemm_v1"), (T64, "w4a4_gemm_v2")):
+        Ww = transform_weights(Wd, w_t).to(torch.bfloat16).cuda().contiguous()
+        wqw, wsw = C.quant_int4(Ww)
+        y = getattr(C, gemm)(q1, s1, wqw, wsw).double().cpu()
+        e = ((y - Yt).norm() / Yt.norm()).item()
+        assert e < 0.10, (gemm, e)
 
 
 def test_p13_graph_capture_replay(C):
