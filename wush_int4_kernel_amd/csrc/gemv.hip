@@ -27,18 +27,12 @@ namespace wush {
 #define WUSH_GEMV_WAVES 4       // wavefronts per workgroup at M = 1 (2 / 8 / 16 no better)
 #endif
 #ifndef WUSH_GEMV_WAVES_M
-#define WUSH_GEMV_WAVES_M 16    // ... for M >= 2: the staged activations (M*K*5/8 bytes of
+#define WUSH_GEMV_WAVES_M 16    // ... for M >= 2: the staged activations (M*K*3/4 bytes of
 #endif                          // LDS) are shared by 16 wavefronts (L70 M=8: 51.5 vs 53.5 us)
 template <int M>
 constexpr int gemv_waves() { return M == 1 ? WUSH_GEMV_WAVES : WUSH_GEMV_WAVES_M; }
 #ifndef WUSH_GEMV_RS
 #define WUSH_GEMV_RS 1          // recursive-halving reduction of the R x M outputs
-#endif
-#ifndef WUSH_GEMV_MAXWAVES
-#define WUSH_GEMV_MAXWAVES 0
-#endif
-#ifndef WUSH_GEMV_INTERLEAVE
-#define WUSH_GEMV_INTERLEAVE 0
 #endif
 #ifndef WUSH_GEMV_TBAR
 #define WUSH_GEMV_TBAR 1        // scheduling barrier after each group (fewer live VGPRs)
@@ -170,17 +164,9 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-#if WUSH_GEMV_INTERLEAVE
-    // chunks of R rows dealt round-robin over the grid's wavefronts
-    (void)rows_per_wave;
-    const int n_begin = (blockIdx.x * gemv_waves<M>() + wave) * R;
-    const int n_step = gridDim.x * gemv_waves<M>() * R;
-    const int n_end = N;
-#else
     const int n_begin = (blockIdx.x * gemv_waves<M>() + wave) * rows_per_wave;
     const int n_step = R;
     const int n_end = min(N, n_begin + rows_per_wave);
-#endif
 
     if constexpr (GPL > 0) {
         using Chunk = GemvChunk<R, GPL>;
@@ -314,16 +300,9 @@ static void launch_gemv_t(const uint8_t* xq, const uint16_t* xs, const uint8_t* 
             per_cu = 2;
         resident_waves = per_cu * kGemvWaves * cus;
     }
-#if WUSH_GEMV_INTERLEAVE
-    const int chunks = (N + R - 1) / R;
-    const int waves = min(WUSH_GEMV_MAXWAVES > 0 ? min(resident_waves, WUSH_GEMV_MAXWAVES) : resident_waves, chunks);
-    const int rows_per_wave = 0;
-    const int blocks = (waves + kGemvWaves - 1) / kGemvWaves;
-#else
     int rows_per_wave = (N + resident_waves - 1) / resident_waves;
     rows_per_wave = max(rows_per_wave, 1);
     const int blocks = (N + kGemvWaves * rows_per_wave - 1) / (kGemvWaves * rows_per_wave);
-#endif
     gemv_int4_kernel<M, R, GPL><<<dim3(blocks), dim3(64 * kGemvWaves), smem, stream>>>(xq, xs, wq, ws, y, N, K,
                                                                                         rows_per_wave);
 }
