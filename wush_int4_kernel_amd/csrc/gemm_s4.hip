@@ -296,6 +296,9 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
 // below).  Weight scales arrive as one 16-byte load per row and
 // stage; the bf16 x scales of the slice sit in LDS.  Requires K % 256 == 0
 // and slices of whole stages.
+#ifndef WUSH_STREAM_EARLY
+#define WUSH_STREAM_EARLY 1      // request the next weights right after the slab write
+#endif
 constexpr int kStreamSG = 8;                     // groups per stage
 constexpr int kStreamPlane = 32 * 8 + 16;        // bytes per (group, half) plane of a 32-row block
 
@@ -375,7 +378,7 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
         for (int j = 0; j < NR; ++j) acc[b][j] = 0.0f;
 
     const int nst = gcount / kStreamSG;
-    auto load = [&](int st, StreamStage<NB>& S) {
+    auto load_w = [&](int st, StreamStage<NB>& S) {
         const size_t off = (size_t)st * (kStreamSG * 16);
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
@@ -386,10 +389,18 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
                 const size_t row_off = ((wmask[b] >> j) & 1u) ? (size_t)j * slice : 0;
                 S.w[b][j] = load_nt16(wp[b] + row_off + off);
             }
-            S.sw[b] = *reinterpret_cast<const uint4*>(sp[b] + st * kStreamSG);
         }
+    };
+    auto load_xs = [&](int st, StreamStage<NB>& S) {
+        const size_t off = (size_t)st * (kStreamSG * 16);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) S.sw[b] = *reinterpret_cast<const uint4*>(sp[b] + st * kStreamSG);
 #pragma unroll
         for (int t = 0; t < 4; ++t) S.x[t] = *reinterpret_cast<const uint4*>(xp + off + (size_t)t * 32);
+    };
+    auto load = [&](int st, StreamStage<NB>& S) {
+        load_w(st, S);
+        load_xs(st, S);
     };
 
     // The first stages' weights do not depend on the staged data: request
@@ -433,8 +444,8 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
     __syncthreads();
     if (nb0 * 32 >= N) return;
 
-    auto process = [&](int st, StreamStage<NB>& S) {
-        // 1. transpose this stage's weights into the slab
+    // 1. transpose a stage's weights into the slab
+    auto to_slab = [&](StreamStage<NB>& S) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
 #pragma unroll
@@ -446,6 +457,8 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
                 *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) = make_uint2(v.z, v.w);
             }
         }
+    };
+    auto compute = [&](int st, StreamStage<NB>& S) {
         // 2. per group: activation operand, weight fragment from the slab, the
         //    two MFMAs (D and the scale products), then the fold.  Software
         //    pipelined: the MFMAs of group g+1 are issued before the fold of
@@ -495,18 +508,34 @@ __global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __re
         }
     };
 
+    // The next stage's weights reuse a stage's registers as soon as they sit
+    // in the slab, before its MFMAs and fold, so two stages of weights stay
+    // in flight while the wavefront computes; its activations and scales
+    // follow the fold.
     int st = 0;
     for (; st + PF <= nst; st += PF) {
 #pragma unroll
         for (int d = 0; d < PF; ++d) {
-            process(st + d, buf[d]);
-            load(min(st + d + PF, nst - 1), buf[d]);
+            const int nx = min(st + d + PF, nst - 1);
+            to_slab(buf[d]);
+#if WUSH_STREAM_EARLY
+            load_w(nx, buf[d]);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(st + d, buf[d]);
+            load_xs(nx, buf[d]);
+#else
+            compute(st + d, buf[d]);
+            load(nx, buf[d]);
+#endif
             __builtin_amdgcn_sched_barrier(0);
         }
     }
 #pragma unroll
     for (int d = 0; d < PF - 1; ++d)
-        if (st + d < nst) process(st + d, buf[d]);
+        if (st + d < nst) {
+            to_slab(buf[d]);
+            compute(st + d, buf[d]);
+        }
 
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -804,6 +833,7 @@ struct Plan {
 #ifndef WUSH_STREAM_PF
 #define WUSH_STREAM_PF 2
 #endif
+
 #ifndef WUSH_STREAM_WAVES
 #define WUSH_STREAM_WAVES 1024   // split K until this many wavefronts stream (measured best)
 #endif
