@@ -122,3 +122,30 @@ def test_cfg4_qwen3_8b_small_batch(C, M):
 def test_cfg5_prefill(C, M, N, K):
     # K=N=4096 at M=4096 and the Llama-70B FFN at M=4096
     _chain_case(C, M, N, K, 500 + N, 16, 1024)
+
+
+@pytest.mark.parametrize("M", [1, 8, 32])
+def test_l70_exact_properties(C, M):
+    # Size-independent properties at the full Llama-70B FFN shape, where the
+    # oracle would be slow: (1) doubling every activation scale doubles every
+    # output exactly (a power-of-two factor passes through the exact group
+    # dots and every fp32 fold and fp16 rounding unchanged); (2) permuting the
+    # weight rows permutes the outputs bit for bit (each output's arithmetic
+    # does not depend on where its row sits); (3) zero weight rows give zeros.
+    import torch
+    N, K = 57344, 8192
+    g = rng(700 + M)
+    W = _dev_weights(N, K, 700 + M)
+    wq, ws = C.quant_int4(W)
+    del W
+    xq, xs = C.quant_int4(to_dev_bf16(outlier_activations(g, M, K)))
+    y = C.w4a4_gemm_s4(xq, xs, wq, ws)
+    y2 = C.w4a4_gemm_s4(xq, (xs.float() * 2).to(torch.bfloat16), wq, ws)
+    assert torch.equal(y2, y * 2), M
+    perm = torch.from_numpy(g.permutation(N)).cuda()
+    yp = C.w4a4_gemm_s4(xq, xs, wq[perm].contiguous(), ws[perm].contiguous())
+    assert torch.equal(yp, y[:, perm]), M
+    wz = wq.clone()
+    wz[::97] = 0
+    yz = C.w4a4_gemm_s4(xq, xs, wz, ws)
+    assert (yz[:, ::97] == 0).all() and torch.equal(yz[:, 1::97], y[:, 1::97]), M
