@@ -64,8 +64,33 @@ __device__ __forceinline__ int code_of(float v, float sf) {
     return (y == y) ? (int)r : 0;
 }
 
+// RN(v / sf) without a division: r = RN(1/sf) once per group, then two fma
+// corrections of q0 = RN(v*r).  q0 is within 1.5 ulps of v/sf and sf has 8
+// significant bits, so each remainder v - q*sf is exactly representable and
+// fma computes it exactly; q1 is then within an ulp of v/sf, and Markstein's
+// theorem (r = RN(1/sf), q1 faithful, exact remainder) makes
+// q2 = RN(q1 + e1*r) = RN(v/sf).  Requires finite v with |v| < 1.8e19 and a
+// normal sf >= 1e-8 (no overflow); below 2^-100 a remainder may underflow,
+// but such quotients are far below 0.5 and give code 0 either way.
+// tests/native/quant_codes_fp32.c checks quotients and codes against the
+// division at and next to every rounding tie and on random operands.
+__device__ __forceinline__ float quotient_fma(float v, float sf, float r) {
+    const float q0 = v * r;
+    const float e0 = __builtin_fmaf(-q0, sf, v);
+    const float q1 = __builtin_fmaf(e0, r, q0);
+    const float e1 = __builtin_fmaf(-q1, sf, v);
+    return __builtin_fmaf(e1, r, q1);
+}
+
+// code + 8 in [1, 15] as a float, from a quotient (rint, +8 exact, clamp).
+__device__ __forceinline__ float code8_of_quotient(float q) {
+    return __builtin_amdgcn_fmed3f(__builtin_rintf(q) + 8.0f, 1.0f, 15.0f);
+}
+
 // Quantize 32 fp32 values in registers: sequential sums, scale, 16 packed
 // bytes as 4 dwords (element 2k low nibble of byte k).
+// A group whose sum of squares is finite takes the division-free quotient;
+// one with an inf or NaN element (s2 not finite) keeps code_of's division.
 __device__ __forceinline__ uint32_t quant_group32(const float (&v)[32], uint32_t (&w)[4]) {
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
@@ -75,13 +100,29 @@ __device__ __forceinline__ uint32_t quant_group32(const float (&v)[32], uint32_t
     }
     float sf;
     uint32_t sb = group_scale(s1, s2, &sf);
+    if (!__builtin_isfinite(s2)) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            uint32_t acc = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                acc |= (uint32_t)(code_of(v[d * 8 + e], sf) & 0xF) << (4 * e);
+            w[d] = acc;
+        }
+        return sb;
+    }
+    const float r = 1.0f / sf;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-        uint32_t acc = 0;
+        // even elements 8d+2k -> byte k of a, odd ones -> byte k of b; the
+        // bytes hold code + 8, an xor with 8 makes them two's complement nibbles
+        uint32_t a = 0, b = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            acc |= (uint32_t)(code_of(v[d * 8 + e], sf) & 0xF) << (4 * e);
-        w[d] = acc;
+        for (int k = 0; k < 4; ++k) {
+            a = __builtin_amdgcn_cvt_pk_u8_f32(code8_of_quotient(quotient_fma(v[8 * d + 2 * k], sf, r)), k, a);
+            b = __builtin_amdgcn_cvt_pk_u8_f32(code8_of_quotient(quotient_fma(v[8 * d + 2 * k + 1], sf, r)), k, b);
+        }
+        w[d] = (a ^ 0x08080808u) | ((b ^ 0x08080808u) << 4);
     }
     return sb;
 }
