@@ -259,6 +259,27 @@ def test_decode_ops_route_to_either_kernel(C, M):
         assert rel_fro(f16_tensor_f64(y1[:, cols]), ref) < 2e-3, (M, N, K)
 
 
+def test_rtn_int4_module_on_gpu(C):
+    # my_int4.rtn_int4 (reference my_int4/rtn_int4.py:33-75): quant_int4 is
+    # the bit-exact kernel, dequant_int4 decodes like the oracle, and
+    # w4a4_matmul_reference is the group-scaled product within the 2e-3 bar
+    import torch
+    from my_int4 import rtn_int4
+    g = rng(8)
+    xb = _bf16(g, (3, 5, 128))
+    wb = _bf16(g, (96, 128), 0.02)
+    xq, xs = rtn_int4.quant_int4(to_dev_bf16(xb))
+    wq, ws = rtn_int4.quant_int4(to_dev_bf16(wb))
+    qo, so = oracle.quant(xb, "bf16")
+    assert np.array_equal(xq.cpu().numpy(), qo) and np.array_equal(bf16_tensor_bits(xs), so)
+    d = rtn_int4.dequant_int4(xq, xs).cpu().numpy()
+    assert np.array_equal(d.reshape(-1, 128), oracle.dequant(qo.reshape(-1, 64), so.reshape(-1, 4)).astype(np.float32))
+    y = rtn_int4.w4a4_matmul_reference(xq, xs, wq, ws)
+    assert tuple(y.shape) == (3, 5, 96) and y.dtype == torch.float16
+    ref = oracle.gemm_f64(qo.reshape(-1, 64), so.reshape(-1, 4), wq.cpu().numpy(), bf16_tensor_bits(ws))
+    assert rel_fro(f16_tensor_f64(y.reshape(-1, 96)), ref) < 2e-3
+
+
 def test_s4_atom_selftest(C):
     import torch
     g = rng(7)

@@ -116,3 +116,25 @@ def test_torch_ops_reject_cpu_tensors():
             getattr(_C, op)(q, s, q, s)
     with pytest.raises(RuntimeError, match="CUDA"):
         _C.w4a4_gemm_cutlass(q, q, 1.0)
+
+
+def test_reference_python_modules_exposed():
+    # reference my_int4/rtn_int4.py and my_int4/wush_transform.py: same names
+    # and parameters; rtn_int4's quant/product refuse CPU tensors (no CPU path)
+    import inspect
+    import torch
+    from my_int4 import rtn_int4, wush_transform
+    assert list(inspect.signature(rtn_int4.quant_int4).parameters) == ["x", "group_size"]
+    assert list(inspect.signature(rtn_int4.dequant_int4).parameters) == ["q_byte", "scale", "group_size"]
+    assert list(inspect.signature(rtn_int4.w4a4_matmul_reference).parameters) == ["x_q", "x_s", "w_q", "w_s"]
+    for name in ("compute_wush_transform", "transform_weights", "transform_activations_reference"):
+        assert callable(getattr(wush_transform, name))
+    assert list(inspect.signature(wush_transform.compute_wush_transform).parameters)[:4] == \
+        ["X_cal", "W", "group_size", "use_hadamard"]
+    with pytest.raises(RuntimeError, match="GPU"):
+        rtn_int4.quant_int4(torch.zeros(2, 64, dtype=torch.bfloat16))
+    # dequant decodes the packed format: byte 0xD3 = codes (+3, -3), scale 0.5
+    q = torch.tensor([[0xD3] * 16], dtype=torch.uint8)
+    s = torch.tensor([[0.5]], dtype=torch.bfloat16)
+    d = rtn_int4.dequant_int4(q, s)
+    assert d.shape == (1, 32) and d[0, 0].item() == 1.5 and d[0, 1].item() == -1.5
