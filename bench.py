@@ -68,9 +68,89 @@ def parse():
     ap.add_argument("--N", type=int, default=N_L70)
     ap.add_argument("--counter-workload", action="store_true",
                     help="launch every kernel of the path 3 times, then a 512 MiB copy (rocprofv3 --pmc)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="the reference's shape x M matrix (bench/exp_p13_matrix.py): a table, one JSON line")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only launch the M=1 dominant kernel (for rocprofv3 runs)")
     return ap.parse_args()
+
+
+SWEEP_SHAPES = [("Qwen3-8B", 4096, 4096), ("Qwen3-8B", 4096, 24576), ("Qwen3-8B", 12288, 4096),
+                ("Llama-70B", 8192, 8192), ("Llama-70B", 8192, 57344)]
+SWEEP_MS = [1, 2, 4, 8, 16, 32, 64, 128, 256, 1024, 2048, 4096]
+
+
+def sweep(args):
+    """The reference's performance matrix (bench/exp_p13_matrix.py:64-73): five
+    FFN shapes x M = 1..4096, the layer step of my_int4.chain (its dispatch by
+    M) against hipBLASLt fp16 (the reference's baseline) and bf16, all captured
+    --graph-steps steps per HIP graph over enough distinct weight copies to
+    exceed the 256 MB MALL (the reference replays one warm weight set)."""
+    import torch
+    from my_int4 import _C
+    from my_int4.chain import make_chain
+    from wush_int4_kernel_amd.wush_transform import compute_wush_transform, transform_weights
+
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.preferred_blas_library("hipblaslt")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    rows = []
+
+    def capture(fns):
+        for _ in range(2):
+            for fn in fns:
+                fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for fn in fns:
+                fn()
+        return g
+
+    def timed(g, steps_per_replay, replays):
+        g.replay()
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for _ in range(replays):
+            g.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t) / (replays * steps_per_replay)
+
+    for model, K, N in SWEEP_SHAPES:
+        W = (torch.randn(N, K, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        Xc = torch.randn(256, K, generator=gen, device=dev)
+        T64 = compute_wush_transform(Xc.double(), W.double())
+        wq, ws = _C.quant_int4(transform_weights(W.double(), T64).to(torch.bfloat16).contiguous())
+        T = T64.to(torch.bfloat16).contiguous()
+        ncopies = max(2, min(8, -(-300_000_000 // (N * K * 9 // 16))))
+        copies = [(wq, ws, T)] + [(wq.clone(), ws.clone(), T.clone()) for _ in range(ncopies - 1)]
+        nb = max(2, min(8, -(-300_000_000 // (N * K * 2))))
+        blas_w = [W] + [W.clone() for _ in range(nb - 1)]
+        half_w = [w.half() for w in blas_w]
+        for M in SWEEP_MS:
+            X = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+            gs = args.graph_steps
+            reps = max(1, int(2e-3 / max(1e-6, 2 * M * N * K / 1e15) / gs) + 1) if M > 64 else 20
+            g = capture([make_chain(X, c[2], c[0], c[1], M) for c in (copies[i % ncopies] for i in range(gs))])
+            t4 = timed(g, gs, reps)
+            del g
+            gb = capture([lambda Wc=blas_w[i % nb]: torch.matmul(X, Wc.t()) for i in range(gs)])
+            tb = timed(gb, gs, reps)
+            del gb
+            X16 = X.half()
+            gh = capture([lambda Wc=half_w[i % nb]: torch.matmul(X16, Wc.t()) for i in range(gs)])
+            th = timed(gh, gs, reps)
+            del gh
+            tf = 2 * M * N * K / 1e12
+            rows.append({"model": model, "K": K, "N": N, "M": M, "int4_us": round(t4 * 1e6, 2),
+                         "int4_tflops": round(tf / t4, 2), "hipblaslt_fp16_us": round(th * 1e6, 2),
+                         "hipblaslt_bf16_us": round(tb * 1e6, 2), "speedup_vs_fp16": round(th / t4, 3),
+                         "speedup_vs_bf16": round(tb / t4, 3)})
+            log(f"{model:9s} K={K:5d} N={N:5d} M={M:5d} | int4 {t4 * 1e6:9.2f} us {tf / t4:7.1f} TF/s | "
+                f"fp16 {th * 1e6:9.2f} us | bf16 {tb * 1e6:9.2f} us | {th / t4:5.2f}x {tb / t4:5.2f}x")
+        del copies, blas_w, half_w, W, wq, ws
+        torch.cuda.empty_cache()
+    print(json.dumps({"sweep": "reference shape x M matrix (bench/exp_p13_matrix.py)", "rows": rows}))
 
 
 def layer_bytes(M, N, K):
@@ -102,6 +182,9 @@ def main():
                           "multi-GPU mode (it would shard the weight rows along N, column-"
                           "parallel, with one all-gather of y); run with --gpus 1"}))
         sys.exit(2)
+
+    if args.sweep:
+        return sweep(args)
 
     import torch
     from my_int4 import _C
