@@ -320,10 +320,10 @@ def test_gemm_decode_many_row_blocks(capi, M):
 @pytest.mark.parametrize("M", [1, 8, 17, 32])
 def test_gemm_scale_alignment_paths_agree(capi, M):
     # Scales that are only 2-byte aligned take the LDS-tiled kernel, 16-byte
-    # aligned ones a streaming kernel (decode M, K % 256 == 0).  For M > 8
-    # both fold the same exact group dots in the same group order: equal bit
-    # for bit.  The M <= 8 streaming kernel sums even and odd groups in two
-    # chains, so there the two agree to fp16 rounding only.
+    # aligned ones a streaming kernel (decode M, K % 256 == 0).  Both fold the
+    # same exact group dots; the streaming kernels sum them in another order
+    # (even/odd group chains at M <= 8, per-wavefront K slices added in
+    # wavefront order above), so the two agree to fp16 rounding.
     import torch
     g = rng(4250 + M)
     N, K = 300, 1024
@@ -342,10 +342,37 @@ def test_gemm_scale_alignment_paths_agree(capi, M):
         torch.cuda.synchronize()
         outs.append(f16_tensor_f64(y))
         assert rel_fro(outs[-1], ref) < FRO_TOL, (M, shift, rel_fro(outs[-1], ref))
-    if M > 8:
-        assert np.array_equal(outs[0], outs[1])
-    else:
-        assert rel_fro(outs[1], outs[0]) < 1e-3
+    assert rel_fro(outs[1], outs[0]) < 1e-3
+
+
+@pytest.mark.parametrize("M,K", [(9, 256), (16, 512), (24, 768), (32, 1024)])
+def test_gemm_stream_group_dots_exact_per_group(capi, M, K):
+    # The streaming kernels (16-byte aligned scales, K % 256 == 0): scales 1
+    # on group g only and 0 elsewhere -> y = D[:, :, g] exactly, whichever
+    # wavefront of the K split holds group g.
+    g = rng(4210 + M)
+    N = 40
+    xq, _, wq, _ = _rand_operands(g, M, N, K)
+    D = oracle.group_dots(xq, wq)
+    for gg in range(K // 32):
+        xs = np.zeros((M, K // 32), np.uint16)
+        ws = np.zeros((N, K // 32), np.uint16)
+        xs[:, gg] = 0x3F80
+        ws[:, gg] = 0x3F80
+        y = run_gemm(capi, xq, xs, wq, ws)
+        assert np.array_equal(y, D[:, :, gg].astype(np.float64)), (M, K, gg)
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 33, 256), (12, 4097, 768), (17, 70, 2048), (31, 1000, 1280),
+                                   (32, 8192, 4096), (20, 96, 8192)])
+def test_gemm_stream_k_split_shapes(capi, M, N, K):
+    # in-workgroup K split: stage counts that leave some wavefronts idle
+    # (K = 256, 768), ragged N, and global split-K on top (small N, long K)
+    g = rng(4280 + M + N)
+    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    y = run_gemm(capi, xq, xs, wq, ws)
+    ref = oracle.gemm_f64(xq, xs, wq, ws)
+    assert rel_fro(y, ref) < FRO_TOL, (M, N, K, rel_fro(y, ref))
 
 
 def test_gemm_golden_fixture(capi):

@@ -281,24 +281,15 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
         }
 }
 
-// ------------------------------------------------ streaming kernel (M <= 32)
-// Decode-sized M: the run time is the weight stream, so each wavefront owns
-// 32*NB weight rows and streams its K slice with PF stages (8 groups = one
-// 128-byte line per row) of loads in flight in registers -- under full load
-// HBM needs ~150-200 KB outstanding per CU.  A stage of weights is read with
-// fully coalesced loads (lane i: row 8j + i/8, line chunk i%8) and transposed
+// ---------------------------------------------------- streaming kernels
+// Decode-sized M: the run time is the weight stream.  A stage is 8 groups
+// (one 128-byte line per weight row).  Its weights are read with fully
+// coalesced loads (lane i: row 8j + i/8, line chunk i%8) and transposed
 // through a wavefront-private LDS slab into the MFMA operand layout
-// [group][k-half][row][8 B]; the slab's plane stride (272 B) makes both the
-// transposing writes and the fragment reads bank-conflict-free, and no
-// workgroup barrier is needed.  Activations (<= 32 rows, L2-resident) are
-// loaded as whole 16-byte groups and re-paired across lane halves with
-// v_permlane32_swap (M <= 8 has its own kernel, gemm_s4_stream8_kernel,
-// below).  Weight scales arrive as one 16-byte load per row and
-// stage; the bf16 x scales of the slice sit in LDS.  Requires K % 256 == 0
-// and slices of whole stages.
-#ifndef WUSH_STREAM_EARLY
-#define WUSH_STREAM_EARLY 1      // request the next weights right after the slab write
-#endif
+// [group][k-half][row][8 B]; the slab's plane stride (272 B for 32 rows)
+// makes both the transposing writes and the fragment reads bank-conflict-free,
+// and no workgroup barrier is needed.  Requires K % 256 == 0 and slices of
+// whole stages.
 constexpr int kStreamSG = 8;                     // groups per stage
 constexpr int kStreamPlane = 32 * 8 + 16;        // bytes per (group, half) plane of a 32-row block
 
@@ -313,250 +304,241 @@ __device__ __forceinline__ void swap_halves(uint4& v) {
     v.y = b[0]; v.w = b[1];
 }
 
-template <int NB>
-struct StreamStage {
-    uint4 w[NB][4];     // weight line chunks: row 8j + lane/8, group lane%8
+// ---------------------------- streaming kernel, 8 < M <= 32, K split in-workgroup
+// One workgroup per 32-row weight block (and global K slice); its KW
+// wavefronts take the slice's stages round-robin (wavefront w: stages w,
+// w + KW, ...), so KW neighbouring 128-byte lines of every row are in flight
+// together and a Llama-70B FFN layer (N = 57344) runs 7168 wavefronts -- 7 per
+// SIMD, evenly -- where one wavefront per block gives 1792, i.e. 1 or 2 per
+// SIMD with the fold work of two on the busiest ones.  Per stage a wavefront
+// loads the block's weights (coalesced, transposed through its LDS slab), the
+// activations (whole 16-byte groups, re-paired
+// with v_permlane32_swap) and, per lane, 16 bytes of bf16 scales for its
+// activation row and its weight column.  Addresses are a wave-uniform base
+// plus a 32-bit lane offset (no 64-bit address arithmetic per load).
+//
+// Fold factors: the bf16 MFMA takes the lane's 8 activation scales of the
+// stage as they were loaded and a weight-scale operand holding only group g's
+// scale (the other 7 elements zero), so each factor is 2*sx[g]*sw[g] exactly.
+// The four weight operands (one per scale dword) keep their zero elements in
+// registers across the loop: one AND per group builds an operand.  A
+// non-finite activation scale meets a zero and gives NaN for its whole row,
+// as the reference's dequantized product does (code 0 * inf scale).
+// Groups are software pipelined: group g+1's two MFMAs are issued before
+// group g's fold.  At the end the KW partial accumulators go through LDS and
+// are summed in wavefront order (deterministic).  Requires K % 256 == 0,
+// 16-byte aligned scales and slices of whole stages.
+template <int MR>
+struct Stream32Stage {
+    uint4 w[4];         // weight line chunks: row 8j + lane/8, group lane%8
     uint4 x[4];         // activation groups 2t + half of row lane%32
-    uint4 sw[NB];       // 8 bf16 weight scales of this lane's column
+    uint4 sx;           // 8 bf16 activation scales of row lane%32
+    uint4 sw;           // 8 bf16 weight scales of column lane%32
 };
 
-template <int MR, int NB, int PF>
-__global__ __launch_bounds__(256) void gemm_s4_stream_kernel(const uint8_t* __restrict__ xq,
-                                                             const uint16_t* __restrict__ xs,
-                                                             const uint8_t* __restrict__ wq,
-                                                             const uint16_t* __restrict__ ws,
-                                                             uint16_t* __restrict__ y,
-                                                             float* __restrict__ partial,
-                                                             int M, int N, int K, int groups_per_split) {
+template <int MR, int KW, int PF, int OCC>
+__global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(OCC)))
+void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq,
+                                                                  const uint16_t* __restrict__ xs,
+                                                                  const uint8_t* __restrict__ wq,
+                                                                  const uint16_t* __restrict__ ws,
+                                                                  uint16_t* __restrict__ y,
+                                                                  float* __restrict__ partial,
+                                                                  int M, int N, int K, int groups_per_split) {
     constexpr int NR = MR / 2;
-    constexpr int kSlab = NB * kStreamSG * 2 * kStreamPlane;    // bytes of one wavefront's slab
-    constexpr int XR = 32;                       // activation rows staged per group
-    static_assert(MR % 8 == 0 && MR <= 32, "fold rows");
+    constexpr int kSlab = kStreamSG * 2 * kStreamPlane;
+    static_assert(MR % 8 == 0 && MR <= 32 && NR % KW == 0, "fold rows");
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform (readfirstlane): the stage loop is uniform control flow
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int half = lane >> 5;
     const int l32 = lane & 31;
     const int G = K >> 5;
     const int K2 = K >> 1;
     const int g_begin = blockIdx.y * groups_per_split;
     const int g_end = min(G, g_begin + groups_per_split);
-    const int gcount = g_end - g_begin;          // multiple of kStreamSG
-    uint16_t* sx_l = reinterpret_cast<uint16_t*>(smem);                    // bf16 [gcount][XR]
-    uint8_t* slab = smem + (size_t)groups_per_split * XR * sizeof(uint16_t) + (size_t)wave * kSlab;
+    const int nst = (g_end - g_begin) / kStreamSG;
+    const int cnt = nst > wave ? (nst - wave + KW - 1) / KW : 0;   // stages of this wavefront
+    const int n0 = blockIdx.x * 32;
+    uint8_t* slab = smem + (size_t)wave * kSlab;
 
-    // Wavefronts past the last row block (only in the last workgroup) stream
-    // clamped rows and store nothing.
-    const int nb0 = (blockIdx.x * 4 + wave) * NB;
-
-    // Per-lane base pointers; out-of-range rows are clamped to valid rows and
-    // their data masked, so the streaming loop has no branches.  The four
-    // 8-row slices of a 32-row block are one base plus j*8 rows.
-    const uint8_t* wp[NB];
-    uint32_t wmask[NB];
-    const uint16_t* sp[NB];
-    const size_t slice = (size_t)8 * K2;
+    // Uniform bases; rows past N read the block's row 0 and activation rows
+    // past M read row 0 (their outputs are never stored), so the loop has no
+    // branches.
+    const uint8_t* wbase = wq + (size_t)n0 * K2 + (size_t)g_begin * 16;
+    const uint16_t* swbase = ws + (size_t)n0 * G + g_begin;
+    const uint8_t* xbase = xq + (size_t)g_begin * 16;
+    const uint16_t* sxbase = xs + g_begin;
+    const int nvalid = N - n0;
+    uint32_t woff[4];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const int n_first = (nb0 + b) * 32 + (lane >> 3);
-        const int nvalid = N - (nb0 + b) * 32;            // rows of this block that exist
-        uint32_t m = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) m |= (8 * j + (lane >> 3) < nvalid ? 1u : 0u) << j;
-        wmask[b] = m;
-        const int nc = n_first < N ? n_first : N - 1;
-        wp[b] = wq + (size_t)nc * K2 + (size_t)(g_begin + (lane & 7)) * 16;
-        const int n = (nb0 + b) * 32 + l32;
-        sp[b] = ws + (size_t)(n < N ? n : N - 1) * G + g_begin;
+    for (int j = 0; j < 4; ++j) {
+        const int r = 8 * j + (lane >> 3);
+        woff[j] = (uint32_t)(r < nvalid ? r : 0) * (uint32_t)K2 + (uint32_t)(lane & 7) * 16u;
     }
-    const uint8_t* xp = xq + (size_t)(l32 < M ? l32 : 0) * K2 + (size_t)(g_begin + half) * 16;
+    const uint32_t swoff = (uint32_t)(l32 < nvalid ? l32 : 0) * (uint32_t)G;
+    const int mrow = l32 < M ? l32 : 0;
+    const uint32_t xoff = (uint32_t)mrow * (uint32_t)K2 + (uint32_t)half * 16u;
+    const uint32_t sxoff = (uint32_t)mrow * (uint32_t)G;
 
-    float acc[NB][NR];
+    float acc[NR];
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
+    for (int j = 0; j < NR; ++j) acc[j] = 0.0f;
+    // weight-scale operands: quad p carries scale dword p, the rest stay zero
+    v4i fb[4];
 #pragma unroll
-        for (int j = 0; j < NR; ++j) acc[b][j] = 0.0f;
+    for (int p = 0; p < 4; ++p) fb[p] = (v4i){0, 0, 0, 0};
 
-    const int nst = gcount / kStreamSG;
-    auto load_w = [&](int st, StreamStage<NB>& S) {
-        const size_t off = (size_t)st * (kStreamSG * 16);
+    auto stage_of = [&](int i) { return wave + i * KW; };
+    auto load_w = [&](int st, Stream32Stage<MR>& S) {
+        const uint8_t* b = wbase + (size_t)st * (kStreamSG * 16);
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
+        for (int j = 0; j < 4; ++j) S.w[j] = load_nt16(b + woff[j]);
+    };
+    auto load_xs = [&](int st, Stream32Stage<MR>& S) {
+        const uint8_t* b = xbase + (size_t)st * (kStreamSG * 16);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                // rows past N re-read the block's first valid rows; they only
-                // feed output columns >= N, which are never stored
-                const size_t row_off = ((wmask[b] >> j) & 1u) ? (size_t)j * slice : 0;
-                S.w[b][j] = load_nt16(wp[b] + row_off + off);
-            }
+        for (int t = 0; t < 4; ++t) S.x[t] = *reinterpret_cast<const uint4*>(b + xoff + t * 32);
+        S.sx = *reinterpret_cast<const uint4*>(sxbase + st * kStreamSG + sxoff);
+        S.sw = *reinterpret_cast<const uint4*>(swbase + st * kStreamSG + swoff);
+    };
+    auto to_slab = [&](const Stream32Stage<MR>& S) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint4 v = S.w[j];
+            const int row = 8 * j + (lane >> 3), g = lane & 7;
+            uint8_t* base = slab + row * 8;
+            *reinterpret_cast<uint2*>(base + (g * 2 + 0) * kStreamPlane) = make_uint2(v.x, v.y);
+            *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) = make_uint2(v.z, v.w);
         }
     };
-    auto load_xs = [&](int st, StreamStage<NB>& S) {
-        const size_t off = (size_t)st * (kStreamSG * 16);
+    auto compute = [&](Stream32Stage<MR>& S) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) S.sw[b] = *reinterpret_cast<const uint4*>(sp[b] + st * kStreamSG);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) S.x[t] = *reinterpret_cast<const uint4*>(xp + off + (size_t)t * 32);
-    };
-    auto load = [&](int st, StreamStage<NB>& S) {
-        load_w(st, S);
-        load_xs(st, S);
-    };
-
-    // The first stages' weights do not depend on the staged data: request
-    // them before the staging so their HBM latency overlaps it.
-    StreamStage<NB> buf[PF];
-#pragma unroll
-    for (int d = 0; d < PF; ++d) load(min(d, nst - 1), buf[d]);
-
-    // Stage the slice's x scales in LDS.
-    // All of a thread's loads are issued before its LDS stores, so the
-    // staging costs one L2 round trip, not one per element.
-    {
-        // one 16-byte load = the scales of 8 consecutive groups of one row
-        constexpr int U = XR / 8;
-        const int nchunk = XR * (gcount >> 3);
-        for (int c0 = threadIdx.x; c0 < nchunk; c0 += 256 * U) {
-            uint4 v[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int c = c0 + u * 256;
-                const int m = c % XR, gc = c / XR;
-                v[u] = (c < nchunk && m < M)
-                           ? *reinterpret_cast<const uint4*>(xs + (size_t)m * G + g_begin + gc * 8)
-                           : make_uint4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int c = c0 + u * 256;
-                if (c < nchunk) {
-                    const int m = c % XR, gc = c / XR;
-                    const uint32_t* h = &v[u].x;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        sx_l[(gc * 8 + 2 * e) * XR + m] = (uint16_t)(h[e] & 0xffffu);
-                        sx_l[(gc * 8 + 2 * e + 1) * XR + m] = (uint16_t)(h[e] >> 16);
-                    }
-                }
-            }
-        }
-    }
-    __syncthreads();
-    if (nb0 * 32 >= N) return;
-
-    // 1. transpose a stage's weights into the slab
-    auto to_slab = [&](StreamStage<NB>& S) {
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint4 v = S.w[b][j];
-                const int row = 8 * j + (lane >> 3), g = lane & 7;
-                uint8_t* base = slab + b * (kStreamSG * 2 * kStreamPlane) + row * 8;
-                *reinterpret_cast<uint2*>(base + (g * 2 + 0) * kStreamPlane) = make_uint2(v.x, v.y);
-                *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) = make_uint2(v.z, v.w);
-            }
-        }
-    };
-    auto compute = [&](int st, StreamStage<NB>& S) {
-        // 2. per group: activation operand, weight fragment from the slab, the
-        //    two MFMAs (D and the scale products), then the fold.  Software
-        //    pipelined: the MFMAs of group g+1 are issued before the fold of
-        //    group g, so the fold overlaps the MFMA latency of the next group.
-        const int gi0 = st * kStreamSG;
-        uint4 xv[kStreamSG / 2];
-#pragma unroll
-        for (int t = 0; t < kStreamSG / 2; ++t) {
-            xv[t] = S.x[t];                      // rows >= M duplicate row 0: outputs not stored
-            swap_halves(xv[t]);
-        }
-        auto issue = [&](int g, v16i (&d)[NB], v16f (&sc)[NB]) {
-            uint32_t a0, a1, a2, a3;
-            unpack_s4x8_x16((g & 1) ? xv[g >> 1].z : xv[g >> 1].x, a0, a1);
-            unpack_s4x8_x16((g & 1) ? xv[g >> 1].w : xv[g >> 1].y, a2, a3);
+        for (int t = 0; t < kStreamSG / 2; ++t) swap_halves(S.x[t]);   // rows >= M: not stored
+        const v4i fa = {(int)S.sx.x, (int)S.sx.y, (int)S.sx.z, (int)S.sx.w};
+        const uint32_t* sww = &S.sw.x;
+        auto issue = [&](int g, v16i& d, v16f& f) {
+            const uint4& xv = S.x[g >> 1];
+            uint32_t a0, a1, a2, a3, b0, b1, b2, b3;
+            unpack_s4x8_x16((g & 1) ? xv.z : xv.x, a0, a1);
+            unpack_s4x8_x16((g & 1) ? xv.w : xv.y, a2, a3);
+            const uint2 w = *reinterpret_cast<const uint2*>(slab + (g * 2 + half) * kStreamPlane + l32 * 8);
+            unpack_s4x8_x16(w.x, b0, b1);
+            unpack_s4x8_x16(w.y, b2, b3);
             const v4i A = {(int)a0, (int)a1, (int)a2, (int)a3};
-            const uint32_t sxb = sx_l[(gi0 + g) * XR + l32];
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const uint2 w = *reinterpret_cast<const uint2*>(
-                    slab + b * (kStreamSG * 2 * kStreamPlane) + (g * 2 + half) * kStreamPlane + l32 * 8);
-                uint32_t b0, b1, b2, b3;
-                unpack_s4x8_x16(w.x, b0, b1);
-                unpack_s4x8_x16(w.y, b2, b3);
-                const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
-                const uint32_t sw2 = (&S.sw[b].x)[g >> 1];
-                const uint32_t swb = (g & 1) ? (sw2 >> 16) : (sw2 & 0xffffu);
-                d[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (v16i){0}, 0, 0, 0);
-                sc[b] = scale_products(sxb, swb);
-            }
+            const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
+            v4i& fbg = fb[g >> 1];
+            fbg[g >> 1] = (int)(sww[g >> 1] & ((g & 1) ? 0xffff0000u : 0x0000ffffu));
+            d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (v16i){0}, 0, 0, 0);
+            f = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa),
+                                                        __builtin_bit_cast(bf16x8, fbg), (v16f){0.0f}, 0, 0, 0);
         };
-        v16i d0[NB], d1[NB];
-        v16f s0[NB], s1[NB];
-        issue(0, d0, s0);
+        auto fold = [&](const v16i& d, const v16f& f) {
+#pragma unroll
+            for (int j = 0; j < NR; ++j) acc[j] = __builtin_fmaf((float)d[j], f[j], acc[j]);
+        };
+        v16i d0, d1;
+        v16f f0, f1;
+        issue(0, d0, f0);
 #pragma unroll
         for (int g = 0; g < kStreamSG; g += 2) {
-            issue(g + 1, d1, s1);
-#pragma unroll
-            for (int b = 0; b < NB; ++b)
-#pragma unroll
-                for (int j = 0; j < NR; ++j) acc[b][j] = __builtin_fmaf((float)d0[b][j], s0[b][j], acc[b][j]);
-            if (g + 2 < kStreamSG) issue(g + 2, d0, s0);
-#pragma unroll
-            for (int b = 0; b < NB; ++b)
-#pragma unroll
-                for (int j = 0; j < NR; ++j) acc[b][j] = __builtin_fmaf((float)d1[b][j], s1[b][j], acc[b][j]);
+            issue(g + 1, d1, f1);
+            fold(d0, f0);
+            if (g + 2 < kStreamSG) issue(g + 2, d0, f0);
+            fold(d1, f1);
         }
     };
 
-    // The next stage's weights reuse a stage's registers as soon as they sit
-    // in the slab, before its MFMAs and fold, so two stages of weights stay
-    // in flight while the wavefront computes; its activations and scales
-    // follow the fold.
-    int st = 0;
-    for (; st + PF <= nst; st += PF) {
+    // PF stages of this wavefront in flight: the next weights reuse a stage's
+    // registers as soon as they sit in the slab, before its MFMAs and fold.
+    Stream32Stage<MR> buf[PF];
+#pragma unroll
+    for (int d = 0; d < PF; ++d)
+        if (d < cnt) {
+            load_w(stage_of(d), buf[d]);
+            load_xs(stage_of(d), buf[d]);
+        }
+    // Steady state: every load is needed (no clamped re-reads, and no
+    // conditional loads in the loop, which would keep stale stage registers
+    // live across it).
+    int i = 0;
+    for (; i + 2 * PF <= cnt; i += PF) {
 #pragma unroll
         for (int d = 0; d < PF; ++d) {
-            const int nx = min(st + d + PF, nst - 1);
             to_slab(buf[d]);
-#if WUSH_STREAM_EARLY
-            load_w(nx, buf[d]);
+            load_w(stage_of(i + d + PF), buf[d]);
             __builtin_amdgcn_sched_barrier(0);
-            compute(st + d, buf[d]);
-            load_xs(nx, buf[d]);
-#else
-            compute(st + d, buf[d]);
-            load(nx, buf[d]);
-#endif
+            compute(buf[d]);
+            load_xs(stage_of(i + d + PF), buf[d]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
+    // Drain: r < 2*PF stages left, the first min(r, PF) of them in buf.  The
+    // buffers are consumed inside each branch, so no stage registers stay
+    // live across a conditional load.
+    const int r = cnt - i;
+    if (r > PF) {
+        // one more pipelined pass; a load past the last stage re-reads it
 #pragma unroll
-    for (int d = 0; d < PF - 1; ++d)
-        if (st + d < nst) {
+        for (int d = 0; d < PF; ++d) {
+            const int nx = min(i + d + PF, cnt - 1);
             to_slab(buf[d]);
-            compute(st + d, buf[d]);
+            load_w(stage_of(nx), buf[d]);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(buf[d]);
+            load_xs(stage_of(nx), buf[d]);
+            __builtin_amdgcn_sched_barrier(0);
         }
-
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const int col = (nb0 + b) * 32 + l32;
-        if (col >= N) continue;
-#pragma unroll
-        for (int j = 0; j < NR; ++j) {
-            const int row = 8 * (j >> 2) + 4 * half + (j & 3);
-            if (row < M) {
-                const float v = acc[b][j] * kFoldOutScale;
-                if (partial != nullptr)
-                    partial[((size_t)blockIdx.y * M + row) * N + col] = v;
-                else
-                    y[(size_t)row * N + col] = f32_to_f16_bits(v);
+        for (int d = 0; d < PF - 1; ++d)
+            if (d < r - PF) {
+                to_slab(buf[d]);
+                compute(buf[d]);
             }
+    } else {
+#pragma unroll
+        for (int d = 0; d < PF; ++d)
+            if (d < r) {
+                to_slab(buf[d]);
+                compute(buf[d]);
+            }
+    }
+
+    // Sum the KW partial accumulators in wavefront order; wavefront w stores
+    // accumulator registers w*NR/KW .. (w+1)*NR/KW - 1.
+    __syncthreads();                                   // every slab is consumed
+    float* red = reinterpret_cast<float*>(smem);       // [KW][NR][64]
+#pragma unroll
+    for (int j = 0; j < NR; ++j) red[(wave * NR + j) * 64 + lane] = acc[j];
+    __syncthreads();
+    constexpr int JW = NR / KW;
+    const int col = n0 + l32;
+#pragma unroll
+    for (int u = 0; u < JW; ++u) {
+        const int j = wave * JW + u;
+        float v = red[j * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < KW; ++w) v += red[(w * NR + j) * 64 + lane];
+        const int row = 8 * (j >> 2) + 4 * half + (j & 3);
+        if (row < M && col < N) {
+            v *= kFoldOutScale;
+            if (partial != nullptr)
+                partial[((size_t)blockIdx.y * M + row) * N + col] = v;
+            else
+                y[(size_t)row * N + col] = f32_to_f16_bits(v);
         }
     }
 }
 
+constexpr size_t stream32_smem(int kw, int nr) {
+    return (size_t)kw * kStreamSG * 2 * kStreamPlane > (size_t)kw * nr * 64 * 4
+               ? (size_t)kw * kStreamSG * 2 * kStreamPlane
+               : (size_t)kw * nr * 64 * 4;
+}
+
 // ------------------------------------------ streaming kernel, M <= 8
-// Same weight stream and slab as gemm_s4_stream_kernel, but the MFMA is
+// Same weight stream and slab as gemm_s4_stream32_kernel, but the MFMA is
 // v_mfma_i32_16x16x64_i8 over a pair of groups with a block-diagonal
 // activation operand: MFMA row (m, e) = m + 8e carries activation row m's
 // codes of group 2p+e in k 32e..32e+31 and zeros in the other half, so D row
@@ -823,34 +805,26 @@ __global__ void mfma_selftest_kernel(const int8_t* __restrict__ a, const int8_t*
 
 // ---------------------------------------------------------------- planning
 struct Plan {
-    int cfg;        // 0: 32x128 (M <= 32), 1: 64x128, 2: 128x128, 3: streaming (M <= 32)
-    int mr;         // fold rows per 32-row block (cfg 0)
+    int cfg;        // 0: 32x128 (M <= 32), 1: 64x128, 2: 128x128, 3: streaming (M <= 8),
+                    // 4: streaming with in-workgroup K split (8 < M <= 32)
+    int mr;         // fold rows per 32-row block (cfg 0, 4)
     int splits;
     int groups_per_split;
     int tm, tn, sg;
 };
 
-#ifndef WUSH_STREAM_PF
-#define WUSH_STREAM_PF 2
-#endif
-
 #ifndef WUSH_STREAM_WAVES
-#define WUSH_STREAM_WAVES 1024   // split K until this many wavefronts stream (measured best)
+#define WUSH_STREAM_WAVES 1024   // M <= 8: split K until this many wavefronts stream (measured best)
 #endif
-#ifndef WUSH_STREAM_NB
-#define WUSH_STREAM_NB 1
-#endif
-constexpr int kStreamNB = WUSH_STREAM_NB;      // 32-row weight blocks per wavefront
-constexpr int kStreamPF = WUSH_STREAM_PF;        // stages of loads in flight per wavefront
 #ifndef WUSH_STREAM_PFX
 #define WUSH_STREAM_PFX 2
 #endif
-constexpr int kStreamPFX = WUSH_STREAM_PFX;      // same, M <= 8 kernel
+constexpr int kStreamPFX = WUSH_STREAM_PFX;      // stages in flight per wavefront, M <= 8 kernel
 constexpr size_t kStreamLdsMax = 64 * 1024;
 
-// LDS bytes of a streaming launch with gps groups per slice: M <= 8 stages
-// x scales (4 B per group pair and row) and codes (128 B per group) plus the
-// zero words; M > 8 stages bf16 x scales of 32 rows.  Plus the four slabs.
+// LDS bytes of an M <= 8 streaming launch with gps groups per slice: the
+// staged x scales (4 B per group pair and row) and codes (128 B per group),
+// the zero words, and the slabs.
 // Geometry of the M <= 8 kernel: 16 weight rows per wavefront (twice the
 // wavefronts of 32-row ones, which keeps more HBM requests in flight) and 8
 // wavefronts per workgroup sharing the staged activations.  Measured at L70:
@@ -864,47 +838,89 @@ constexpr size_t kStreamLdsMax = 64 * 1024;
 #define WUSH_S8_WPB 8            // its wavefronts per workgroup
 #endif
 constexpr int kS8Rows = 16 * WUSH_S8_NH;
-static size_t stream_smem(int64_t gps, bool m8) {
-    if (m8)
-        return (size_t)gps * (16 + 128) + kStream8ZeroBytes +
-               (size_t)WUSH_S8_WPB * kStreamSG * 2 * (kS8Rows * 8 + 16);
-    return (size_t)gps * 32 * sizeof(uint16_t) + 4 * (size_t)kStreamNB * kStreamSG * 2 * kStreamPlane;
+static size_t stream8_smem(int64_t gps) {
+    return (size_t)gps * (16 + 128) + kStream8ZeroBytes + (size_t)WUSH_S8_WPB * kStreamSG * 2 * (kS8Rows * 8 + 16);
 }
 
-// scales16: both scale tensors are 16-byte aligned (the streaming kernel reads
-// them 8 groups at a time).
 #ifndef WUSH_PF_BM
 #define WUSH_PF_BM 2             // prefill tile: 32x32 blocks per wavefront along M
 #endif
 #ifndef WUSH_PF_BN
 #define WUSH_PF_BN 2             // and along N (2 x 2 wavefronts per workgroup)
 #endif
+// 8 < M <= 32 streaming kernel (gemm_s4_stream32_kernel).  Measured on
+// MI355X against one wavefront per 32-row block: L70 (K=8192, N=57344)
+// M = 16 / 24 / 32: 64 / 70 / 80 us against 67 / 75 / 80; Qwen3-8B FFN
+// (K=4096, N=24576) M = 16 / 32: 15.3 / 19.7 us against 23.0 / 30.0.
+#ifndef WUSH_S32_KW
+#define WUSH_S32_KW 4            // wavefronts per workgroup (= K ways; 2 was slower at every shape)
+#endif
+#ifndef WUSH_S32_PF16
+#define WUSH_S32_PF16 1          // stages in flight per wavefront, M <= 16
+#endif
+#ifndef WUSH_S32_OCC16
+#define WUSH_S32_OCC16 4         // ... and the wavefronts per SIMD its registers allow
+#endif
+#ifndef WUSH_S32_PF32
+#define WUSH_S32_PF32 1          // the same for 16 < M <= 32 (L70 M=24: 69.7 us with 1 stage
+#endif                           // and 3 wavefronts per SIMD, 76.7 with 2 and 2)
+#ifndef WUSH_S32_OCC32
+#define WUSH_S32_OCC32 3
+#endif
+#ifndef WUSH_S32_WAVES
+#define WUSH_S32_WAVES 2048      // split K across workgroups below this many wavefronts
+#endif
+constexpr int kStream32KW = WUSH_S32_KW;
+constexpr int kStream32Waves = WUSH_S32_WAVES;
+
+// scales16: both scale tensors are 16-byte aligned (the streaming kernels
+// read them 8 groups at a time).
 static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available, bool allow_split,
                       bool scales16) {
     Plan p;
     p.mr = 32;
     const int64_t G0 = K / 32;
-    if (allow_split && scales16 && M <= 32 && K % 256 == 0) {
-        // streaming kernel: one wavefront per 32*kStreamNB weight rows
-        p.cfg = 3; p.tm = 32; p.tn = 4 * kStreamNB * 32; p.sg = kStreamSG;
+    if (allow_split && scales16 && M > 8 && M <= 32 && K % 256 == 0) {
+        // in-workgroup K split: one workgroup of kStream32KW wavefronts per
+        // 32-row block; split K across workgroups only while fewer than
+        // kStream32Waves wavefronts would stream and every wavefront keeps
+        // at least two stages
+        p.cfg = 4; p.tm = 32; p.tn = 32; p.sg = kStreamSG;
         p.mr = (int)((M + 7) / 8 * 8);
-        const int rows_per_wave = M <= 8 ? kS8Rows : 32 * kStreamNB;
-        p.tn = (M <= 8 ? WUSH_S8_WPB : 4) * rows_per_wave;
-        const int64_t waves = (N + rows_per_wave - 1) / rows_per_wave;
-        static_assert(kStreamNB == 1, "the M <= 8 kernel streams one 32-row block per wavefront");
+        const int64_t wgs = (N + 31) / 32;
+        int s = 1;
+        while (s < 16 && wgs * s * kStream32KW < kStream32Waves &&
+               G0 / (2 * s) >= (int64_t)kStream32KW * 2 * kStreamSG)
+            s *= 2;
+        int64_t gps = (G0 + s - 1) / s;
+        gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
+        s = (int)((G0 + gps - 1) / gps);
+        if (s > 1 && (size_t)s * (size_t)M * (size_t)N * sizeof(float) > ws_bytes_available) {
+            s = 1;                               // no room for partials: one slice
+            gps = G0;
+        }
+        p.splits = s;
+        p.groups_per_split = (int)gps;
+        return p;
+    }
+    if (allow_split && scales16 && M <= 8 && K % 256 == 0) {
+        // M <= 8 streaming kernel: one wavefront per kS8Rows weight rows
+        p.cfg = 3; p.tm = 32; p.sg = kStreamSG;
+        p.mr = 8;
+        p.tn = WUSH_S8_WPB * kS8Rows;
+        const int64_t waves = (N + kS8Rows - 1) / kS8Rows;
         int s = 1;
         while (s < 16 && waves * s < WUSH_STREAM_WAVES && G0 / (2 * s) >= 4 * kStreamSG) s *= 2;
         int64_t gps = (G0 + s - 1) / s;
         gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
-        const bool m8 = p.mr == 8;
-        while (stream_smem(gps, m8) > kStreamLdsMax && gps > kStreamSG) {
+        while (stream8_smem(gps) > kStreamLdsMax && gps > kStreamSG) {
             s *= 2;
             gps = (G0 + s - 1) / s;
             gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
         }
         s = (int)((G0 + gps - 1) / gps);
         const bool ws_ok = s == 1 || (size_t)s * (size_t)M * (size_t)N * sizeof(float) <= ws_bytes_available;
-        if (ws_ok && stream_smem(gps, m8) <= kStreamLdsMax) {
+        if (ws_ok && stream8_smem(gps) <= kStreamLdsMax) {
             p.splits = s;
             p.groups_per_split = (int)gps;
             return p;
@@ -960,19 +976,34 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     WUSH_REQUIRE((N + p.tn - 1) / p.tn <= 0x7fffffffLL && (M + p.tm - 1) / p.tm <= 65535);
     float* partial = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int m = (int)M, n = (int)N, k = (int)K;
-    if (p.cfg == 3) {
+    if (p.cfg == 4) {
         if constexpr (!PT) {
-            const size_t smem = stream_smem(p.groups_per_split, p.mr == 8);
-            dim3 grid((unsigned)((N + p.tn - 1) / p.tn), (unsigned)p.splits);
+            dim3 grid((unsigned)((N + 31) / 32), (unsigned)p.splits);
+            constexpr int KW = kStream32KW;
             switch (p.mr) {
-                case 8:
-                    gemm_s4_stream8_kernel<kStreamPFX, WUSH_S8_NH, WUSH_S8_WPB><<<grid, 64 * WUSH_S8_WPB, smem, stream>>>(
-                        xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
+                case 16:
+                    gemm_s4_stream32_kernel<16, KW, WUSH_S32_PF16, WUSH_S32_OCC16>
+                        <<<grid, 64 * KW, stream32_smem(KW, 8), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
+                                                                          p.groups_per_split);
                     break;
-                case 16: gemm_s4_stream_kernel<16, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
-                case 24: gemm_s4_stream_kernel<24, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
-                default: gemm_s4_stream_kernel<32, kStreamNB, kStreamPF><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split); break;
+                case 24:
+                    gemm_s4_stream32_kernel<24, KW, WUSH_S32_PF32, WUSH_S32_OCC32>
+                        <<<grid, 64 * KW, stream32_smem(KW, 12), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
+                                                                           p.groups_per_split);
+                    break;
+                default:
+                    gemm_s4_stream32_kernel<32, KW, WUSH_S32_PF32, WUSH_S32_OCC32>
+                        <<<grid, 64 * KW, stream32_smem(KW, 16), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
+                                                                           p.groups_per_split);
+                    break;
             }
+        }
+    } else if (p.cfg == 3) {
+        if constexpr (!PT) {
+            const size_t smem = stream8_smem(p.groups_per_split);
+            dim3 grid((unsigned)((N + p.tn - 1) / p.tn), (unsigned)p.splits);
+            gemm_s4_stream8_kernel<kStreamPFX, WUSH_S8_NH, WUSH_S8_WPB><<<grid, 64 * WUSH_S8_WPB, smem, stream>>>(
+                xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
         }
     } else if (p.cfg == 0) {
         if (PT || p.mr == 32)
