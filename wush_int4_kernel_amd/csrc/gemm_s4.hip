@@ -328,6 +328,9 @@ __device__ __forceinline__ void swap_halves(uint4& v) {
 // group g's fold.  At the end the KW partial accumulators go through LDS and
 // are summed in wavefront order (deterministic).  Requires K % 256 == 0,
 // 16-byte aligned scales and slices of whole stages.
+#ifndef WUSH_S32_NT
+#define WUSH_S32_NT 1            // non-temporal weight loads
+#endif
 template <int MR>
 struct Stream32Stage {
     uint4 w[4];         // weight line chunks: row 8j + lane/8, group lane%8
@@ -347,7 +350,7 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq,
                                                                   int M, int N, int K, int groups_per_split) {
     constexpr int NR = MR / 2;
     constexpr int kSlab = kStreamSG * 2 * kStreamPlane;
-    static_assert(MR % 8 == 0 && MR <= 32 && NR % KW == 0, "fold rows");
+    static_assert(MR % 8 == 0 && MR <= 32, "fold rows");
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     // wave-uniform (readfirstlane): the stage loop is uniform control flow
@@ -394,7 +397,13 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq,
     auto load_w = [&](int st, Stream32Stage<MR>& S) {
         const uint8_t* b = wbase + (size_t)st * (kStreamSG * 16);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) S.w[j] = load_nt16(b + woff[j]);
+        for (int j = 0; j < 4; ++j) {
+#if WUSH_S32_NT
+            S.w[j] = load_nt16(b + woff[j]);
+#else
+            S.w[j] = *reinterpret_cast<const uint4*>(b + woff[j]);
+#endif
+        }
     };
     auto load_xs = [&](int st, Stream32Stage<MR>& S) {
         const uint8_t* b = xbase + (size_t)st * (kStreamSG * 16);
@@ -506,17 +515,14 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq,
     }
 
     // Sum the KW partial accumulators in wavefront order; wavefront w stores
-    // accumulator registers w*NR/KW .. (w+1)*NR/KW - 1.
+    // accumulator registers w, w + KW, ...
     __syncthreads();                                   // every slab is consumed
     float* red = reinterpret_cast<float*>(smem);       // [KW][NR][64]
 #pragma unroll
     for (int j = 0; j < NR; ++j) red[(wave * NR + j) * 64 + lane] = acc[j];
     __syncthreads();
-    constexpr int JW = NR / KW;
     const int col = n0 + l32;
-#pragma unroll
-    for (int u = 0; u < JW; ++u) {
-        const int j = wave * JW + u;
+    for (int j = wave; j < NR; j += KW) {
         float v = red[j * 64 + lane];
 #pragma unroll
         for (int w = 1; w < KW; ++w) v += red[(w * NR + j) * 64 + lane];
@@ -853,8 +859,11 @@ static size_t stream8_smem(int64_t gps) {
 // M = 16 / 24 / 32: 64 / 70 / 80 us against 67 / 75 / 80; Qwen3-8B FFN
 // (K=4096, N=24576) M = 16 / 32: 15.3 / 19.7 us against 23.0 / 30.0.
 #ifndef WUSH_S32_KW
-#define WUSH_S32_KW 4            // wavefronts per workgroup (= K ways; 2 was slower at every shape)
-#endif
+#define WUSH_S32_KW 8            // wavefronts per workgroup (= K ways) at M <= 16 and 24 < M
+#endif                           // (L70 M=32: 77.9 us with 8, 80.3 with 4; 2 was slower everywhere)
+#ifndef WUSH_S32_KW24
+#define WUSH_S32_KW24 4          // ... at 16 < M <= 24: 137 VGPRs allow 12 wavefronts per CU, one
+#endif                           // 8-wavefront workgroup (L70 M=24: 69.0 us with 4, 73.0 with 8)
 #ifndef WUSH_S32_PF16
 #define WUSH_S32_PF16 1          // stages in flight per wavefront, M <= 16
 #endif
@@ -864,13 +873,16 @@ static size_t stream8_smem(int64_t gps) {
 #ifndef WUSH_S32_PF32
 #define WUSH_S32_PF32 1          // the same for 16 < M <= 32 (L70 M=24: 69.7 us with 1 stage
 #endif                           // and 3 wavefronts per SIMD, 76.7 with 2 and 2)
+#ifndef WUSH_S32_OCC24
+#define WUSH_S32_OCC24 3
+#endif
 #ifndef WUSH_S32_OCC32
-#define WUSH_S32_OCC32 3
+#define WUSH_S32_OCC32 4         // (128 VGPRs either way with the 2-deep group pipeline)
 #endif
 #ifndef WUSH_S32_WAVES
 #define WUSH_S32_WAVES 2048      // split K across workgroups below this many wavefronts
 #endif
-constexpr int kStream32KW = WUSH_S32_KW;
+constexpr int stream32_kw(int mr) { return mr == 24 ? WUSH_S32_KW24 : WUSH_S32_KW; }
 constexpr int kStream32Waves = WUSH_S32_WAVES;
 
 // scales16: both scale tensors are 16-byte aligned (the streaming kernels
@@ -881,16 +893,16 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
     p.mr = 32;
     const int64_t G0 = K / 32;
     if (allow_split && scales16 && M > 8 && M <= 32 && K % 256 == 0) {
-        // in-workgroup K split: one workgroup of kStream32KW wavefronts per
+        // in-workgroup K split: one workgroup of stream32_kw wavefronts per
         // 32-row block; split K across workgroups only while fewer than
         // kStream32Waves wavefronts would stream and every wavefront keeps
         // at least two stages
         p.cfg = 4; p.tm = 32; p.tn = 32; p.sg = kStreamSG;
         p.mr = (int)((M + 7) / 8 * 8);
+        const int kw = stream32_kw(p.mr);
         const int64_t wgs = (N + 31) / 32;
         int s = 1;
-        while (s < 16 && wgs * s * kStream32KW < kStream32Waves &&
-               G0 / (2 * s) >= (int64_t)kStream32KW * 2 * kStreamSG)
+        while (s < 16 && wgs * s * kw < kStream32Waves && G0 / (2 * s) >= (int64_t)kw * 2 * kStreamSG)
             s *= 2;
         int64_t gps = (G0 + s - 1) / s;
         gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
@@ -979,23 +991,28 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     if (p.cfg == 4) {
         if constexpr (!PT) {
             dim3 grid((unsigned)((N + 31) / 32), (unsigned)p.splits);
-            constexpr int KW = kStream32KW;
             switch (p.mr) {
-                case 16:
+                case 16: {
+                    constexpr int KW = stream32_kw(16);
                     gemm_s4_stream32_kernel<16, KW, WUSH_S32_PF16, WUSH_S32_OCC16>
                         <<<grid, 64 * KW, stream32_smem(KW, 8), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
                                                                           p.groups_per_split);
                     break;
-                case 24:
-                    gemm_s4_stream32_kernel<24, KW, WUSH_S32_PF32, WUSH_S32_OCC32>
+                }
+                case 24: {
+                    constexpr int KW = stream32_kw(24);
+                    gemm_s4_stream32_kernel<24, KW, WUSH_S32_PF32, WUSH_S32_OCC24>
                         <<<grid, 64 * KW, stream32_smem(KW, 12), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
                                                                            p.groups_per_split);
                     break;
-                default:
+                }
+                default: {
+                    constexpr int KW = stream32_kw(32);
                     gemm_s4_stream32_kernel<32, KW, WUSH_S32_PF32, WUSH_S32_OCC32>
                         <<<grid, 64 * KW, stream32_smem(KW, 16), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
                                                                            p.groups_per_split);
                     break;
+                }
             }
         }
     } else if (p.cfg == 3) {
