@@ -317,10 +317,10 @@ def test_gemm_decode_many_row_blocks(capi, M):
     assert rel_fro(y, ref) < FRO_TOL, (M, rel_fro(y, ref))
 
 
-@pytest.mark.parametrize("M", [1, 8, 17, 32])
+@pytest.mark.parametrize("M", [1, 8, 17, 32, 40, 64])
 def test_gemm_scale_alignment_paths_agree(capi, M):
     # Scales that are only 2-byte aligned take the LDS-tiled kernel, 16-byte
-    # aligned ones a streaming kernel (decode M, K % 256 == 0).  Both fold the
+    # aligned ones a streaming kernel (M <= 64, K % 256 == 0).  Both fold the
     # same exact group dots; the streaming kernels sum them in another order
     # (even/odd group chains at M <= 8, per-wavefront K slices added in
     # wavefront order above), so the two agree to fp16 rounding.
@@ -345,7 +345,7 @@ def test_gemm_scale_alignment_paths_agree(capi, M):
     assert rel_fro(outs[1], outs[0]) < 1e-3
 
 
-@pytest.mark.parametrize("M,K", [(9, 256), (16, 512), (24, 768), (32, 1024)])
+@pytest.mark.parametrize("M,K", [(9, 256), (16, 512), (24, 768), (32, 1024), (48, 512), (64, 256)])
 def test_gemm_stream_group_dots_exact_per_group(capi, M, K):
     # The streaming kernels (16-byte aligned scales, K % 256 == 0): scales 1
     # on group g only and 0 elsewhere -> y = D[:, :, g] exactly, whichever
@@ -364,7 +364,8 @@ def test_gemm_stream_group_dots_exact_per_group(capi, M, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(9, 33, 256), (12, 4097, 768), (17, 70, 2048), (31, 1000, 1280),
-                                   (32, 8192, 4096), (20, 96, 8192)])
+                                   (32, 8192, 4096), (20, 96, 8192), (33, 500, 512), (40, 1000, 1024),
+                                   (57, 33, 256), (64, 4096, 2048)])
 def test_gemm_stream_k_split_shapes(capi, M, N, K):
     # in-workgroup K split: stage counts that leave some wavefronts idle
     # (K = 256, 768), ragged N, and global split-K on top (small N, long K)

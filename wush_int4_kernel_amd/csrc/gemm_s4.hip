@@ -328,29 +328,27 @@ __device__ __forceinline__ void swap_halves(uint4& v) {
 // group g's fold.  At the end the KW partial accumulators go through LDS and
 // are summed in wavefront order (deterministic).  Requires K % 256 == 0,
 // 16-byte aligned scales and slices of whole stages.
-#ifndef WUSH_S32_NT
-#define WUSH_S32_NT 1            // non-temporal weight loads
-#endif
-template <int MR>
+template <int MB>
 struct Stream32Stage {
     uint4 w[4];         // weight line chunks: row 8j + lane/8, group lane%8
-    uint4 x[4];         // activation groups 2t + half of row lane%32
-    uint4 sx;           // 8 bf16 activation scales of row lane%32
+    uint4 x[MB][4];     // per activation block b: groups 2t + half of row 32b + lane%32
+    uint4 sx[MB];       // 8 bf16 activation scales of that row
     uint4 sw;           // 8 bf16 weight scales of column lane%32
 };
 
-template <int MR, int KW, int PF, int OCC>
+// MR: rows folded in the last 32-row activation block (8..32); MB: activation
+// blocks per wavefront (1: M <= 32; 2: 32 < M <= 64, the first block full).
+// Both blocks multiply the same staged weights, so the weights stream once.
+template <int MR, int MB, int KW, int PF, int OCC>
 __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(OCC)))
-void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq,
-                                                                  const uint16_t* __restrict__ xs,
-                                                                  const uint8_t* __restrict__ wq,
-                                                                  const uint16_t* __restrict__ ws,
-                                                                  uint16_t* __restrict__ y,
-                                                                  float* __restrict__ partial,
-                                                                  int M, int N, int K, int groups_per_split) {
-    constexpr int NR = MR / 2;
+void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restrict__ xs,
+                             const uint8_t* __restrict__ wq, const uint16_t* __restrict__ ws,
+                             uint16_t* __restrict__ y, float* __restrict__ partial, int M, int N, int K,
+                             int groups_per_split) {
+    constexpr int NRL = MR / 2;                  // accumulator registers of the last block
+    constexpr int NA = 16 * (MB - 1) + NRL;      // accumulator registers in all
     constexpr int kSlab = kStreamSG * 2 * kStreamPlane;
-    static_assert(MR % 8 == 0 && MR <= 32, "fold rows");
+    static_assert(MR % 8 == 0 && MR <= 32 && (MB == 1 || MB == 2), "fold rows");
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     // wave-uniform (readfirstlane): the stage loop is uniform control flow
@@ -381,38 +379,39 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq,
         woff[j] = (uint32_t)(r < nvalid ? r : 0) * (uint32_t)K2 + (uint32_t)(lane & 7) * 16u;
     }
     const uint32_t swoff = (uint32_t)(l32 < nvalid ? l32 : 0) * (uint32_t)G;
-    const int mrow = l32 < M ? l32 : 0;
-    const uint32_t xoff = (uint32_t)mrow * (uint32_t)K2 + (uint32_t)half * 16u;
-    const uint32_t sxoff = (uint32_t)mrow * (uint32_t)G;
-
-    float acc[NR];
+    uint32_t xoff[MB], sxoff[MB];
 #pragma unroll
-    for (int j = 0; j < NR; ++j) acc[j] = 0.0f;
+    for (int b = 0; b < MB; ++b) {
+        const int mrow = 32 * b + l32 < M ? 32 * b + l32 : 0;
+        xoff[b] = (uint32_t)mrow * (uint32_t)K2 + (uint32_t)half * 16u;
+        sxoff[b] = (uint32_t)mrow * (uint32_t)G;
+    }
+
+    float acc[NA];
+#pragma unroll
+    for (int j = 0; j < NA; ++j) acc[j] = 0.0f;
     // weight-scale operands: quad p carries scale dword p, the rest stay zero
     v4i fb[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) fb[p] = (v4i){0, 0, 0, 0};
 
     auto stage_of = [&](int i) { return wave + i * KW; };
-    auto load_w = [&](int st, Stream32Stage<MR>& S) {
+    auto load_w = [&](int st, Stream32Stage<MB>& S) {
         const uint8_t* b = wbase + (size_t)st * (kStreamSG * 16);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#if WUSH_S32_NT
-            S.w[j] = load_nt16(b + woff[j]);
-#else
-            S.w[j] = *reinterpret_cast<const uint4*>(b + woff[j]);
-#endif
-        }
+        for (int j = 0; j < 4; ++j) S.w[j] = load_nt16(b + woff[j]);
     };
-    auto load_xs = [&](int st, Stream32Stage<MR>& S) {
-        const uint8_t* b = xbase + (size_t)st * (kStreamSG * 16);
+    auto load_xs = [&](int st, Stream32Stage<MB>& S) {
+        const uint8_t* bx = xbase + (size_t)st * (kStreamSG * 16);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) S.x[t] = *reinterpret_cast<const uint4*>(b + xoff + t * 32);
-        S.sx = *reinterpret_cast<const uint4*>(sxbase + st * kStreamSG + sxoff);
+        for (int b = 0; b < MB; ++b) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) S.x[b][t] = *reinterpret_cast<const uint4*>(bx + xoff[b] + t * 32);
+            S.sx[b] = *reinterpret_cast<const uint4*>(sxbase + st * kStreamSG + sxoff[b]);
+        }
         S.sw = *reinterpret_cast<const uint4*>(swbase + st * kStreamSG + swoff);
     };
-    auto to_slab = [&](const Stream32Stage<MR>& S) {
+    auto to_slab = [&](const Stream32Stage<MB>& S) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint4 v = S.w[j];
@@ -422,13 +421,15 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq,
             *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) = make_uint2(v.z, v.w);
         }
     };
-    auto compute = [&](Stream32Stage<MR>& S) {
+    auto compute = [&](Stream32Stage<MB>& S) {
 #pragma unroll
-        for (int t = 0; t < kStreamSG / 2; ++t) swap_halves(S.x[t]);   // rows >= M: not stored
-        const v4i fa = {(int)S.sx.x, (int)S.sx.y, (int)S.sx.z, (int)S.sx.w};
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int t = 0; t < kStreamSG / 2; ++t) swap_halves(S.x[b][t]);   // rows >= M: not stored
         const uint32_t* sww = &S.sw.x;
-        auto issue = [&](int g, v16i& d, v16f& f) {
-            const uint4& xv = S.x[g >> 1];
+        // group g, activation block b: D and the fold factors
+        auto issue = [&](int g, int b, v16i& d, v16f& f) {
+            const uint4& xv = S.x[b][g >> 1];
             uint32_t a0, a1, a2, a3, b0, b1, b2, b3;
             unpack_s4x8_x16((g & 1) ? xv.z : xv.x, a0, a1);
             unpack_s4x8_x16((g & 1) ? xv.w : xv.y, a2, a3);
@@ -437,31 +438,47 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq,
             unpack_s4x8_x16(w.y, b2, b3);
             const v4i A = {(int)a0, (int)a1, (int)a2, (int)a3};
             const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
+            const v4i fa = {(int)S.sx[b].x, (int)S.sx[b].y, (int)S.sx[b].z, (int)S.sx[b].w};
             v4i& fbg = fb[g >> 1];
-            fbg[g >> 1] = (int)(sww[g >> 1] & ((g & 1) ? 0xffff0000u : 0x0000ffffu));
+            if (b == 0) fbg[g >> 1] = (int)(sww[g >> 1] & ((g & 1) ? 0xffff0000u : 0x0000ffffu));
             d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (v16i){0}, 0, 0, 0);
             f = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa),
                                                         __builtin_bit_cast(bf16x8, fbg), (v16f){0.0f}, 0, 0, 0);
         };
-        auto fold = [&](const v16i& d, const v16f& f) {
+        auto fold = [&](int b, const v16i& d, const v16f& f) {
+            constexpr int kLast = NRL;
+            const int nr = b == MB - 1 ? kLast : 16;
 #pragma unroll
-            for (int j = 0; j < NR; ++j) acc[j] = __builtin_fmaf((float)d[j], f[j], acc[j]);
+            for (int j = 0; j < 16; ++j)
+                if (j < nr) acc[16 * b + j] = __builtin_fmaf((float)d[j], f[j], acc[16 * b + j]);
         };
         v16i d0, d1;
         v16f f0, f1;
-        issue(0, d0, f0);
+        if constexpr (MB == 1) {
+            // groups pipelined: group g+1's MFMAs are issued before group g's fold
+            issue(0, 0, d0, f0);
 #pragma unroll
-        for (int g = 0; g < kStreamSG; g += 2) {
-            issue(g + 1, d1, f1);
-            fold(d0, f0);
-            if (g + 2 < kStreamSG) issue(g + 2, d0, f0);
-            fold(d1, f1);
+            for (int g = 0; g < kStreamSG; g += 2) {
+                issue(g + 1, 0, d1, f1);
+                fold(0, d0, f0);
+                if (g + 2 < kStreamSG) issue(g + 2, 0, d0, f0);
+                fold(0, d1, f1);
+            }
+        } else {
+            // blocks pipelined: block 1's MFMAs are issued before block 0's fold
+#pragma unroll
+            for (int g = 0; g < kStreamSG; ++g) {
+                issue(g, 0, d0, f0);
+                issue(g, 1, d1, f1);
+                fold(0, d0, f0);
+                fold(1, d1, f1);
+            }
         }
     };
 
     // PF stages of this wavefront in flight: the next weights reuse a stage's
     // registers as soon as they sit in the slab, before its MFMAs and fold.
-    Stream32Stage<MR> buf[PF];
+    Stream32Stage<MB> buf[PF];
 #pragma unroll
     for (int d = 0; d < PF; ++d)
         if (d < cnt) {
@@ -517,16 +534,17 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq,
     // Sum the KW partial accumulators in wavefront order; wavefront w stores
     // accumulator registers w, w + KW, ...
     __syncthreads();                                   // every slab is consumed
-    float* red = reinterpret_cast<float*>(smem);       // [KW][NR][64]
+    float* red = reinterpret_cast<float*>(smem);       // [KW][NA][64]
 #pragma unroll
-    for (int j = 0; j < NR; ++j) red[(wave * NR + j) * 64 + lane] = acc[j];
+    for (int j = 0; j < NA; ++j) red[(wave * NA + j) * 64 + lane] = acc[j];
     __syncthreads();
     const int col = n0 + l32;
-    for (int j = wave; j < NR; j += KW) {
+    for (int j = wave; j < NA; j += KW) {
         float v = red[j * 64 + lane];
 #pragma unroll
-        for (int w = 1; w < KW; ++w) v += red[(w * NR + j) * 64 + lane];
-        const int row = 8 * (j >> 2) + 4 * half + (j & 3);
+        for (int w = 1; w < KW; ++w) v += red[(w * NA + j) * 64 + lane];
+        const int jb = j & 15;
+        const int row = 32 * (j >> 4) + 8 * (jb >> 2) + 4 * half + (jb & 3);
         if (row < M && col < N) {
             v *= kFoldOutScale;
             if (partial != nullptr)
@@ -537,10 +555,10 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq,
     }
 }
 
-constexpr size_t stream32_smem(int kw, int nr) {
-    return (size_t)kw * kStreamSG * 2 * kStreamPlane > (size_t)kw * nr * 64 * 4
+constexpr size_t stream32_smem(int kw, int na) {
+    return (size_t)kw * kStreamSG * 2 * kStreamPlane > (size_t)kw * na * 64 * 4
                ? (size_t)kw * kStreamSG * 2 * kStreamPlane
-               : (size_t)kw * nr * 64 * 4;
+               : (size_t)kw * na * 64 * 4;
 }
 
 // ------------------------------------------ streaming kernel, M <= 8
@@ -882,7 +900,25 @@ static size_t stream8_smem(int64_t gps) {
 #ifndef WUSH_S32_WAVES
 #define WUSH_S32_WAVES 2048      // split K across workgroups below this many wavefronts
 #endif
-constexpr int stream32_kw(int mr) { return mr == 24 ? WUSH_S32_KW24 : WUSH_S32_KW; }
+#ifndef WUSH_S32_MAXM
+#define WUSH_S32_MAXM 64         // largest M of the streaming kernel (64: two activation blocks)
+#endif
+#ifndef WUSH_S32_KW64
+#define WUSH_S32_KW64 4          // K ways at 32 < M <= 64 (168 VGPRs: 12 wavefronts per CU)
+#endif                           // when N > 16384 (L70 M=64: 111 us with 4, 130 with 8) ...
+#ifndef WUSH_S32_KW64S
+#define WUSH_S32_KW64S 8         // ... and when N <= 16384 (K=N=8192 M=64: 21.0 us with 8, 25.4 with 4)
+#endif
+#ifndef WUSH_S32_KW64_N
+#define WUSH_S32_KW64_N 16384
+#endif
+#ifndef WUSH_S32_OCC64
+#define WUSH_S32_OCC64 2
+#endif
+constexpr int kStream32MaxM = WUSH_S32_MAXM;
+constexpr int stream32_kw(int mr, int64_t n = 0) {
+    return mr == 24 ? WUSH_S32_KW24 : mr == 64 ? (n > WUSH_S32_KW64_N ? WUSH_S32_KW64 : WUSH_S32_KW64S) : WUSH_S32_KW;
+}
 constexpr int kStream32Waves = WUSH_S32_WAVES;
 
 // scales16: both scale tensors are 16-byte aligned (the streaming kernels
@@ -892,14 +928,14 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
     Plan p;
     p.mr = 32;
     const int64_t G0 = K / 32;
-    if (allow_split && scales16 && M > 8 && M <= 32 && K % 256 == 0) {
+    if (allow_split && scales16 && M > 8 && M <= kStream32MaxM && K % 256 == 0) {
         // in-workgroup K split: one workgroup of stream32_kw wavefronts per
         // 32-row block; split K across workgroups only while fewer than
         // kStream32Waves wavefronts would stream and every wavefront keeps
         // at least two stages
         p.cfg = 4; p.tm = 32; p.tn = 32; p.sg = kStreamSG;
-        p.mr = (int)((M + 7) / 8 * 8);
-        const int kw = stream32_kw(p.mr);
+        p.mr = M > 32 ? 64 : (int)((M + 7) / 8 * 8);
+        const int kw = stream32_kw(p.mr, N);
         const int64_t wgs = (N + 31) / 32;
         int s = 1;
         while (s < 16 && wgs * s * kw < kStream32Waves && G0 / (2 * s) >= (int64_t)kw * 2 * kStreamSG)
@@ -994,25 +1030,38 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
             switch (p.mr) {
                 case 16: {
                     constexpr int KW = stream32_kw(16);
-                    gemm_s4_stream32_kernel<16, KW, WUSH_S32_PF16, WUSH_S32_OCC16>
+                    gemm_s4_stream32_kernel<16, 1, KW, WUSH_S32_PF16, WUSH_S32_OCC16>
                         <<<grid, 64 * KW, stream32_smem(KW, 8), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
                                                                           p.groups_per_split);
                     break;
                 }
                 case 24: {
                     constexpr int KW = stream32_kw(24);
-                    gemm_s4_stream32_kernel<24, KW, WUSH_S32_PF32, WUSH_S32_OCC24>
+                    gemm_s4_stream32_kernel<24, 1, KW, WUSH_S32_PF32, WUSH_S32_OCC24>
                         <<<grid, 64 * KW, stream32_smem(KW, 12), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
                                                                            p.groups_per_split);
                     break;
                 }
-                default: {
+                case 32: {
                     constexpr int KW = stream32_kw(32);
-                    gemm_s4_stream32_kernel<32, KW, WUSH_S32_PF32, WUSH_S32_OCC32>
+                    gemm_s4_stream32_kernel<32, 1, KW, WUSH_S32_PF32, WUSH_S32_OCC32>
                         <<<grid, 64 * KW, stream32_smem(KW, 16), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
                                                                            p.groups_per_split);
                     break;
                 }
+                default:
+                    if (N > WUSH_S32_KW64_N) {
+                        constexpr int KW = WUSH_S32_KW64;
+                        gemm_s4_stream32_kernel<32, 2, KW, 1, WUSH_S32_OCC64>
+                            <<<grid, 64 * KW, stream32_smem(KW, 32), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
+                                                                               p.groups_per_split);
+                    } else {
+                        constexpr int KW = WUSH_S32_KW64S;
+                        gemm_s4_stream32_kernel<32, 2, KW, 1, WUSH_S32_OCC64>
+                            <<<grid, 64 * KW, stream32_smem(KW, 32), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
+                                                                               p.groups_per_split);
+                    }
+                    break;
             }
         }
     } else if (p.cfg == 3) {
