@@ -23,9 +23,9 @@ hipBLASLt bf16 GEMM time at the same shape measured the same way.
 
 Also reported: the roofline of the dominant kernel at M=1 (gemv_int4, HBM-
 bound; timed alone with HIP events on its launch stream), and the CPU
-baseline -- the project's CPU restatement of the reference path (oracle/:
-rtn quant of x + dequantized fp32 matmul), timed on a bounded sample on this
-host with 1 thread and scaled to the full layer.
+baseline -- the reference's CPU path (rtn quant of x + dequantized fp32
+matmul) restated with the same torch ops in oracle/rtn_torch.py, timed on a
+16384-row weight sample on this host's cores and scaled to the full layer.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -460,22 +460,26 @@ def main():
 
 
 def cpu_baseline(wq, ws, X, N, K):
-    """The reference CPU path on this host: rtn quant of x + dequant of W +
-    fp32 matmul (my_int4/rtn_int4.py:33-75), via the oracle (C, 1 thread) and
-    torch CPU matmul pinned to 1 thread; a 4096-row weight sample, median of
-    5, scaled to the full N."""
-    import numpy as np
+    """The reference CPU path on this host for the L70 layer at M=1: rtn quant
+    of x, dequant of the weights and the fp32 matmul (my_int4/rtn_int4.py:33-75),
+    restated with the same eager torch CPU ops in oracle/rtn_torch.py (bit-
+    identical to the C oracle).  torch runs on the host's cores (at most 16, the
+    box's share per GPU).  Bounded sample: the first 16384 of the N weight rows,
+    median of 5 after a warm-up, scaled by N/16384 (dequant and matmul are
+    linear in N; the x quant is counted once).  A single-thread figure on a
+    2048-row sample is reported beside it."""
     import torch
 
-    import oracle
+    from oracle import rtn_torch
 
-    torch.set_num_threads(1)
-    S = min(4096, N)
-    wq_s = wq[:S].cpu().numpy()
-    ws_s = ws[:S].cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
-    xb = X.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    S = min(16384, N)
+    wq_c = wq[:S].cpu()
+    ws_c = ws[:S].cpu()
+    x_c = X.cpu()
 
     def med(fn, reps=5):
+        fn()
         ts = []
         for _ in range(reps):
             t = time.perf_counter()
@@ -483,14 +487,19 @@ def cpu_baseline(wq, ws, X, N, K):
             ts.append(time.perf_counter() - t)
         return statistics.median(ts)
 
-    oracle.quant(xb, "bf16")
-    t_qx = med(lambda: oracle.quant(xb, "bf16"))
-    xq, xs = oracle.quant(xb, "bf16")
-    xd = torch.from_numpy(oracle.dequant(xq, xs))
-    t_dw = med(lambda: oracle.dequant(wq_s, ws_s))
-    wd = torch.from_numpy(oracle.dequant(wq_s, ws_s))
+    torch.set_num_threads(threads)
+    xq, xs = rtn_torch.quant(x_c)
+    t_qx = med(lambda: rtn_torch.quant(x_c))
+    t_dw = med(lambda: rtn_torch.dequant(wq_c, ws_c))
+    wd = rtn_torch.dequant(wq_c, ws_c)
+    xd = rtn_torch.dequant(xq, xs)
     t_mm = med(lambda: xd @ wd.T)
+    del wd
     per_layer = t_qx + (t_dw + t_mm) * (N / S)
+    S1 = min(2048, N)
+    torch.set_num_threads(1)
+    t1 = t_qx + med(lambda: rtn_torch.w4a4_matmul(xq, xs, wq_c[:S1], ws_c[:S1]), reps=3) * (N / S1)
+    torch.set_num_threads(threads)
     try:
         cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except Exception:
@@ -498,12 +507,13 @@ def cpu_baseline(wq, ws, X, N, K):
     return {
         "value": round(per_layer * 1e6, 1),
         "unit": "us/layer",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"L70 layer M=1: quant(x 1x{K}) + dequant(W {S}x{K} of {N} rows) + fp32 matmul, "
-                  f"median of 5, scaled by N/{S}; quant {t_qx * 1e6:.0f} us, dequant {t_dw * 1e3:.1f} ms, "
-                  f"matmul {t_mm * 1e3:.2f} ms per sample",
-        "host": {"cpu_model": cpu_model, "os_cpu_count": os.cpu_count(), "torch_threads": 1},
+        "sample": f"L70 layer at M=1 (K={K}, N={N}): torch CPU rtn quant of x + dequant of {S} weight rows + "
+                  f"fp32 matmul (oracle/rtn_torch.py, the reference's ops), {threads} threads, median of 5, "
+                  f"scaled by N/{S}; per sample: quant {t_qx * 1e6:.0f} us, dequant {t_dw * 1e3:.1f} ms, "
+                  f"matmul {t_mm * 1e3:.2f} ms; 1 thread: {t1 * 1e3:.0f} ms/layer ({S1}-row sample)",
+        "host": {"cpu_model": cpu_model, "os_cpu_count": os.cpu_count(), "torch_threads": threads},
     }
 
 

@@ -10,7 +10,9 @@ Two independent restatements of the reference semantics live here:
 * ``wush_oracle.c`` (built by ``oracle/Makefile`` into ``oracle/_build/``),
   reached through :mod:`ctypes` -- the fast checker used by the GPU tests;
 * the numpy functions in :mod:`oracle.rtn_np` -- written separately from the C
-  code so the two can be compared bit for bit.
+  code so the two can be compared bit for bit;
+* :mod:`oracle.rtn_torch` -- the reference's eager torch CPU ops, checked bit
+  for bit against the C code; ``bench.py``'s ``cpu_baseline`` leg times it.
 
 Reference semantics followed (paths relative to the reference repo root):
 ``my_int4/rtn_int4.py:15-75`` (quant / dequant / matmul),

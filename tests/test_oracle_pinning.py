@@ -138,6 +138,35 @@ def test_c_and_numpy_restatements_agree():
     assert np.array_equal(q4, q5) and np.array_equal(s4, s5)
 
 
+def test_torch_restatement_matches_c_oracle():
+    # oracle/rtn_torch.py (the CPU baseline's timed path) bit for bit against
+    # the C oracle: outlier activations, ties, overflow, zero, NaN and inf groups
+    import torch
+    from oracle import rtn_torch
+    g = rng(16)
+    x = bf16_bits_to_f32(outlier_activations(g, 32, 1024))
+    special = np.zeros((6, 32), np.float32)
+    special[0] = np.where(np.arange(32) % 2 == 0, 1.0, -1.0)      # test_rtn_int4.py:9-20
+    special[2] = 3.3e38                                            # test_s2.py:31-36
+    special[3, 5] = np.nan
+    special[4, 7] = np.inf
+    special[5] = np.float32(0.35353515625) * (np.arange(32) - 15.5)  # many quotients near ties
+    for arr in (x, special):
+        q1, s1 = oracle.quant(arr)
+        q2, s2 = rtn_torch.quant(torch.from_numpy(arr))
+        assert np.array_equal(q2.numpy(), q1)
+        assert np.array_equal(s2.view(torch.int16).numpy().view(np.uint16), s1)
+        d1 = oracle.dequant(q1, s1)
+        d2 = rtn_torch.dequant(q2, s2).numpy()
+        assert np.array_equal(d1, d2, equal_nan=True)
+    wq, ws = oracle.quant(bf16_bits_to_f32(f32_to_bf16_bits(g.standard_normal((64, 1024)) * 0.02)))
+    xq, xs = oracle.quant(x[:4])
+    y = rtn_torch.w4a4_matmul(torch.from_numpy(xq), torch.from_numpy(xs.view(np.int16)).view(torch.bfloat16),
+                              torch.from_numpy(wq), torch.from_numpy(ws.view(np.int16)).view(torch.bfloat16))
+    ref = oracle.gemm_f64(xq, xs, wq, ws)
+    assert np.abs(y.double().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
 def test_dequant_error_bound_and_shapes():
     # reference tests/test_rtn_int4.py:22-32 (|x - dq| <= 6*scale) and :40-45 (shapes)
     g = rng(14)
