@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
             if (row < TM) {
                 *reinterpret_cast<uint2*>(base + (g * 2 + 0) * S::kAPlane + row * 8) = make_uint2(r.a[c].x, r.a[c].y);
                 *reinterpret_cast<uint2*>(base + (g * 2 + 1) * S::kAPlane + row * 8) = make_uint2(r.a[c].z, r.a[c].w);
-                if constexpr (!PER_TENSOR) sa[g * TM + row] = r.sa[c];
+                if constexpr (!PER_TENSOR) sa[row * SG + g] = r.sa[c];
             }
         }
 #pragma unroll
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
             if (row < TN) {
                 *reinterpret_cast<uint2*>(bbase + (g * 2 + 0) * S::kBPlane + row * 8) = make_uint2(r.b[c].x, r.b[c].y);
                 *reinterpret_cast<uint2*>(bbase + (g * 2 + 1) * S::kBPlane + row * 8) = make_uint2(r.b[c].z, r.b[c].w);
-                if constexpr (!PER_TENSOR) sbp[g * TN + row] = r.sb[c];
+                if constexpr (!PER_TENSOR) sbp[row * SG + g] = r.sb[c];
             }
         }
     };
@@ -184,12 +184,39 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
             iacc[bm][bn] = (v16i){0};
         }
 
+    // weight-scale operands of the fold factors: quad [bn][p] carries scale
+    // dword p (groups 2p, 2p+1), its other dwords stay zero
+    v4i fbq[BN][SG / 2 > 0 ? SG / 2 : 1];
+#pragma unroll
+    for (int bn = 0; bn < BN; ++bn)
+#pragma unroll
+        for (int p = 0; p < (SG / 2 > 0 ? SG / 2 : 1); ++p) fbq[bn][p] = (v4i){0, 0, 0, 0};
+
     auto compute_stage = [&](int buf, int st) {
         const uint8_t* base = smem + buf * S::kBuf;
         const uint8_t* bbase = base + S::kACodes;
         const uint16_t* sa = reinterpret_cast<const uint16_t*>(base + S::kACodes + S::kBCodes);
         const uint16_t* sbp = sa + SG * TM;
         const int groups_here = min(SG, g_end - (g_begin + st * SG));
+        // per-stage scale operands (group-scaled fold only): the SG bf16
+        // scales of this lane's activation row / weight column
+        static_assert(PER_TENSOR || SG == 4 || SG == 8, "scale operand layout");
+        v4i fa[BM];
+        uint32_t swv[BN][SG / 2];
+        if constexpr (!PER_TENSOR) {
+#pragma unroll
+            for (int bm = 0; bm < BM; ++bm) {
+                const uint32_t* p = reinterpret_cast<const uint32_t*>(sa + (wm + bm * 32 + l32) * SG);
+                if constexpr (SG == 4) fa[bm] = (v4i){(int)p[0], (int)p[1], 0, 0};
+                else fa[bm] = (v4i){(int)p[0], (int)p[1], (int)p[2], (int)p[3]};
+            }
+#pragma unroll
+            for (int bn = 0; bn < BN; ++bn) {
+                const uint32_t* p = reinterpret_cast<const uint32_t*>(sbp + (wn + bn * 32 + l32) * SG);
+#pragma unroll
+                for (int e = 0; e < SG / 2; ++e) swv[bn][e] = p[e];
+            }
+        }
 #pragma unroll
         for (int g = 0; g < SG; ++g) {
             if (g >= groups_here) break;
@@ -220,17 +247,23 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
                         iacc[bm][bn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[bm], bfr[bn],
                                                                               iacc[bm][bn], 0, 0, 0);
             } else {
-                uint32_t swb[BN];
+                // fold factors 2*sx*sw: the A operand holds the row's SG
+                // activation scales of the stage (read once per stage), the B
+                // operand only group g's weight scale, its other elements zero
 #pragma unroll
-                for (int bn = 0; bn < BN; ++bn) swb[bn] = sbp[g * TN + wn + bn * 32 + l32];
+                for (int bn = 0; bn < BN; ++bn) {
+                    v4i& q = fbq[bn][g >> 1];
+                    q[g >> 1] = (int)(swv[bn][g >> 1] & ((g & 1) ? 0xffff0000u : 0x0000ffffu));
+                }
 #pragma unroll
                 for (int bm = 0; bm < BM; ++bm) {
-                    const uint32_t sxb = sa[g * TM + wm + bm * 32 + l32];
 #pragma unroll
                     for (int bn = 0; bn < BN; ++bn) {
                         const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(afr[bm], bfr[bn],
                                                                              (v16i){0}, 0, 0, 0);
-                        const v16f sc = scale_products(sxb, swb[bn]);
+                        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            __builtin_bit_cast(bf16x8, fa[bm]), __builtin_bit_cast(bf16x8, fbq[bn][g >> 1]),
+                            (v16f){0.0f}, 0, 0, 0);
 #pragma unroll
                         for (int j = 0; j < NR; ++j)
                             acc[bm][bn][j] = __builtin_fmaf((float)d[j], sc[j], acc[bm][bn][j]);
