@@ -11,7 +11,7 @@ from _util import f16_tensor_f64, f32_to_bf16_bits, outlier_activations, rel_fro
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("M", [1, 3, 4, 5, 8, 32, 33, 300])
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 8, 16, 32, 33, 64, 300])
 def test_make_chain_eager_and_replays(M):
     import torch
     from my_int4.chain import graphed, make_chain
