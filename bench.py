@@ -300,7 +300,7 @@ def main():
             _C.fused_transform_quant_int4(activations(4096, gdev).to(torch.bfloat16), T)
             _C.quant_int4(Wt)
         Wq8, Ws8 = _C.quant_int4((torch.randn(24576, 4096, generator=gdev, device=dev) * 0.02).to(torch.bfloat16))
-        launch_product("gemm", 8, 24576, 4096, Wq8, Ws8)   # Qwen3-8B M=8 (16x16x64 streaming GEMM)
+        launch_product("gemm", 8, 24576, 4096, Wq8, Ws8)   # Qwen3-8B M=8 (K-split streaming GEMM, 8 rows)
         W3, S3 = _C.quant_int4((torch.randn(4096, 4096, generator=gdev, device=dev) * 0.02).to(torch.bfloat16))
         launch_product("gemm", 4096, 4096, 4096, W3, S3)  # 4096^3 prefill tiles
         torch.cuda.synchronize()

@@ -307,8 +307,8 @@ def test_gemm_group_dots_exact_per_group(capi):
 
 @pytest.mark.parametrize("M", [1, 5, 8])
 def test_gemm_decode_many_row_blocks(capi, M):
-    # many row blocks with N not a multiple of 32 or 16: the last workgroup of
-    # the M <= 8 streaming kernel holds a partial block
+    # many row blocks with N not a multiple of 32: the last workgroup of the
+    # streaming kernel holds a partial block
     g = rng(4270 + M)
     N, K = 33000, 512
     xq, xs, wq, ws = _rand_operands(g, M, N, K)
@@ -321,9 +321,9 @@ def test_gemm_decode_many_row_blocks(capi, M):
 def test_gemm_scale_alignment_paths_agree(capi, M):
     # Scales that are only 2-byte aligned take the LDS-tiled kernel, 16-byte
     # aligned ones a streaming kernel (M <= 64, K % 256 == 0).  Both fold the
-    # same exact group dots; the streaming kernels sum them in another order
-    # (even/odd group chains at M <= 8, per-wavefront K slices added in
-    # wavefront order above), so the two agree to fp16 rounding.
+    # same exact group dots; the streaming kernel sums them in another order
+    # (per-wavefront K slices added in wavefront order), so the two agree to
+    # fp16 rounding.
     import torch
     g = rng(4250 + M)
     N, K = 300, 1024
@@ -345,7 +345,8 @@ def test_gemm_scale_alignment_paths_agree(capi, M):
     assert rel_fro(outs[1], outs[0]) < 1e-3
 
 
-@pytest.mark.parametrize("M,K", [(9, 256), (16, 512), (24, 768), (32, 1024), (48, 512), (64, 256)])
+@pytest.mark.parametrize("M,K", [(1, 512), (5, 256), (8, 768), (9, 256), (16, 512), (24, 768), (32, 1024),
+                                 (48, 512), (64, 256)])
 def test_gemm_stream_group_dots_exact_per_group(capi, M, K):
     # The streaming kernels (16-byte aligned scales, K % 256 == 0): scales 1
     # on group g only and 0 elsewhere -> y = D[:, :, g] exactly, whichever

@@ -239,15 +239,16 @@ def test_gemv_ops(C):
         C.w4a4_gemv_multi(xq, xs, wq, ws)
 
 
-@pytest.mark.parametrize("M", [1, 2, 5, 6, 7, 8])
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 6, 7, 8])
 def test_decode_ops_route_to_either_kernel(C, M):
-    # w4a4_gemm_s4 and w4a4_gemv_multi run the dot8 GEMV when its LDS staging
-    # (M*K*3/4 bytes) fits in 64 KiB and the MFMA GEMM otherwise (K = 16384 at
-    # M >= 6).  Either way the two ops give the same product (checked on
-    # sampled columns against the oracle).
+    # w4a4_gemm_s4 and w4a4_gemv_multi run the dot8 GEMV at M <= 4, and at
+    # 5 <= M <= 8 when N > 32768, if its LDS staging (M*K*3/4 bytes) fits in
+    # 64 KiB; otherwise the K-split MFMA GEMM (N = 4096 and 32768 at M >= 5,
+    # K = 16384 at M >= 6).  Either way the two ops give the same product
+    # (checked on sampled columns against the oracle).
     import torch
     g = rng(60 + M)
-    for N, K in [(4096, 4096), (32768, 8192), (1024, 16384)]:
+    for N, K in [(4096, 4096), (32768, 8192), (40000, 4096), (1024, 16384)]:
         wq, ws = C.quant_int4(to_dev_bf16(_bf16(g, (N, K), 0.02)))
         xq, xs = C.quant_int4(to_dev_bf16(_bf16(g, (M, K))))
         cols = torch.from_numpy(np.sort(g.choice(N, size=512, replace=False))).cuda()

@@ -83,8 +83,10 @@ def test_argument_validation_without_device(capi):
 
 
 def test_workspace_plan_is_host_only(capi):
-    # split-K only for skinny shapes with few output tiles
-    assert capi.gemm_s4_workspace_bytes(8, 4096, 4096) > 0
+    # split-K across workgroups only for skinny shapes with few row blocks and
+    # a long K (each wavefront of the in-workgroup K split keeps >= 2 stages)
+    assert capi.gemm_s4_workspace_bytes(8, 1024, 16384) > 0
+    assert capi.gemm_s4_workspace_bytes(8, 4096, 4096) == 0
     assert capi.gemm_s4_workspace_bytes(4096, 4096, 4096) == 0
     assert capi.gemm_s4_workspace_bytes(0, 4096, 4096) == 0
     assert capi.gemm_s4_workspace_bytes(8, 4096, 40) == 0

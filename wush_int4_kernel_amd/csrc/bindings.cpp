@@ -104,16 +104,18 @@ void check_packed(const torch::Tensor& xq, const torch::Tensor& xs, const torch:
 }
 
 // Which kernel family computes a product with M activation rows.  Both give
-// the same math (exact int32 group dots folded in fp32).  Measured on MI355X,
-// the dot8 streaming GEMV (wush_gemv_int4) is faster than the int8-MFMA
-// streaming GEMM (wush_gemm_s4) at every M <= 8 measured (Llama-70B FFN
-// K=8192 N=57344 M=8: 51.1 vs 56.5 us; Qwen3-8B K=4096 N=24576 M=8: 13.9 vs
-// 15.0 us).  The GEMV stages M*K*(1/2 + 1/4) bytes of activation codes and
-// scale terms in LDS, at most 64 KiB; larger M*K take the GEMM.
+// the same math (exact int32 group dots folded in fp32).  Measured on MI355X
+// with the weights streamed from HBM: the dot8 streaming GEMV
+// (wush_gemv_int4) is faster at M <= 4 on every shape and at every M <= 8 on
+// the Llama-70B FFN weights (K=8192 N=57344 M=8: 51.8 vs 55.4 us); the
+// K-split int8-MFMA streaming GEMM (wush_gemm_s4) is faster at 5 <= M <= 8
+// when N <= 24576 (K=N=4096 M=8: 5.8 vs 7.2 us; K=N=8192 M=8: 11.9 vs
+// 13.3 us; K=4096 N=24576 M=8: 14.3 vs 15.0 us).  The GEMV stages
+// M*K*(1/2 + 1/4) bytes of activation codes and scale terms in LDS, at most
+// 64 KiB; larger M*K take the GEMM.
 bool gemv_preferred(int64_t M, int64_t N, int64_t K) {
-    (void)N;
     const bool lds_fits = M * (K / 2) + M * (K / 32) * 8 <= 64 * 1024;
-    return lds_fits && M >= 1 && M <= 8;
+    return lds_fits && M >= 1 && M <= 8 && (M <= 4 || N > 32768);
 }
 
 // Shared product launch: y (M, N) fp16 = group-scaled product.

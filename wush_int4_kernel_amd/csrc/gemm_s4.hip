@@ -49,8 +49,6 @@ __device__ __forceinline__ v16f scale_products(uint32_t sx_bits, uint32_t sw_bit
 // fp32 accumulator -> output: removes the 16*16 of the unpacked codes and the
 // 2 of scale_products.
 constexpr float kFoldOutScale = 1.0f / 512.0f;
-// Same for the 16x16 fold of gemm_s4_stream8_kernel, whose factors are 4*sx*sw.
-constexpr float kFold8OutScale = 1.0f / 1024.0f;
 
 constexpr int kPlanePad = 32;                    // bytes of padding per (group, half) plane
 
@@ -594,234 +592,6 @@ constexpr size_t stream32_smem(int kw, int na) {
                : (size_t)kw * na * 64 * 4;
 }
 
-// ------------------------------------------ streaming kernel, M <= 8
-// Same weight stream and slab as gemm_s4_stream32_kernel, but the MFMA is
-// v_mfma_i32_16x16x64_i8 over a pair of groups with a block-diagonal
-// activation operand: MFMA row (m, e) = m + 8e carries activation row m's
-// codes of group 2p+e in k 32e..32e+31 and zeros in the other half, so D row
-// (m, e) is the exact dot of group 2p+e and no MFMA row is wasted on
-// nonexistent activation rows.  Lane block q = l/16 of either operand holds
-// k 16q..16q+15, i.e. half q%2 of group 2p + q/2.  The fold factors 4*sx*sw
-// come from v_mfma_f32_16x16x16_bf16 (k 4q..4q+3 per lane block): the weight
-// operand is the lane's four bf16 scales of groups 4(p/2)..4(p/2)+3 straight
-// from the scale registers, the activation operand holds sx of row (m, e) at
-// element 2(p%2)+e and zeros elsewhere, so each factor is the sum of four
-// equal exact products.  Even and odd groups accumulate in lanes l and l^32
-// and are added once at the end.
-constexpr int kStream8ZeroBytes = 1024;         // zero words read by off-diagonal lanes
-
-// NH = 16-column halves per wavefront (2: 32 weight rows, 1: 16 rows), WPB =
-// wavefronts per workgroup sharing the staged activations.
-template <int PF, int NH, int WPB>
-__global__ __launch_bounds__(64 * WPB) void gemm_s4_stream8_kernel(const uint8_t* __restrict__ xq,
-                                                              const uint16_t* __restrict__ xs,
-                                                              const uint8_t* __restrict__ wq,
-                                                              const uint16_t* __restrict__ ws,
-                                                              uint16_t* __restrict__ y,
-                                                              float* __restrict__ partial,
-                                                              int M, int N, int K, int groups_per_split) {
-    typedef float v4f __attribute__((ext_vector_type(4)));
-    typedef short v4s __attribute__((ext_vector_type(4)));
-    constexpr int kRows = 16 * NH;               // weight rows per wavefront
-    constexpr int kNW = kRows / 8;               // weight load instructions per stage
-    constexpr int kPlane = kRows * 8 + 16;       // slab plane: kRows x 8 B + pad
-    constexpr int kSlab = kStreamSG * 2 * kPlane;
-    constexpr int kThreads = 64 * WPB;
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int q = lane >> 4;                     // lane block: k 16q..16q+15 of the pair
-    const int r16 = lane & 15;                   // operand row (A: (m, e)) / column (B: n)
-    const int G = K >> 5;
-    const int K2 = K >> 1;
-    const int g_begin = blockIdx.y * groups_per_split;
-    const int g_end = min(G, g_begin + groups_per_split);
-    const int gcount = g_end - g_begin;          // multiple of kStreamSG
-    uint32_t* sx_l = reinterpret_cast<uint32_t*>(smem);              // [gcount/2][8] (even | odd << 16)
-    uint8_t* x_l = smem + (size_t)groups_per_split * 16;             // [gcount][2][8][8 B]
-    uint8_t* x_zero = x_l + (size_t)groups_per_split * 128;          // kStream8ZeroBytes of zeros
-    uint8_t* slab = x_zero + kStream8ZeroBytes + (size_t)wave * kSlab;
-
-    const int nb0 = blockIdx.x * WPB + wave;     // kRows-row weight block of this wavefront
-    const size_t slice = (size_t)8 * K2;
-    uint32_t wmask = 0;
-    {
-        const int nvalid = N - nb0 * kRows;
-#pragma unroll
-        for (int j = 0; j < kNW; ++j) wmask |= (8 * j + (lane >> 3) < nvalid ? 1u : 0u) << j;
-    }
-    const int n_first = nb0 * kRows + (lane >> 3);
-    const uint8_t* wp = wq + (size_t)(n_first < N ? n_first : N - 1) * K2 + (size_t)(g_begin + (lane & 7)) * 16;
-    const uint16_t* sp[NH];
-#pragma unroll
-    for (int h = 0; h < NH; ++h) {
-        const int n = nb0 * kRows + 16 * h + r16;
-        sp[h] = ws + (size_t)(n < N ? n : N - 1) * G + g_begin;
-    }
-
-    struct Stage {
-        uint4 w[kNW];    // weight line chunks: row 8j + lane/8, group lane%8
-        uint4 sw[NH];    // 8 bf16 weight scales of column 16h + r16
-    };
-    const int nst = gcount / kStreamSG;
-    auto load = [&](int st, Stage& S) {
-        const size_t off = (size_t)st * (kStreamSG * 16);
-#pragma unroll
-        for (int j = 0; j < kNW; ++j) {
-            // rows past N re-read the block's first valid rows; they only feed
-            // output columns >= N, which are never stored
-            const size_t row_off = ((wmask >> j) & 1u) ? (size_t)j * slice : 0;
-            S.w[j] = load_nt16(wp + row_off + off);
-        }
-#pragma unroll
-        for (int h = 0; h < NH; ++h) S.sw[h] = *reinterpret_cast<const uint4*>(sp[h] + st * kStreamSG);
-    };
-    // weights first: their HBM latency overlaps the staging below
-    Stage buf[PF];
-#pragma unroll
-    for (int d = 0; d < PF; ++d) load(min(d, nst - 1), buf[d]);
-
-    // Stage x scales (as group pairs), activation codes and the zero words.
-    {
-        const int nchunk = 8 * (gcount >> 3);    // 16-byte loads: 8 groups of one row
-        for (int c = threadIdx.x; c < nchunk; c += kThreads) {
-            const int m = c & 7, gc = c >> 3;
-            const uint4 v = m < M ? *reinterpret_cast<const uint4*>(xs + (size_t)m * G + g_begin + gc * 8)
-                                  : make_uint4(0, 0, 0, 0);
-            sx_l[(gc * 4 + 0) * 8 + m] = v.x;
-            sx_l[(gc * 4 + 1) * 8 + m] = v.y;
-            sx_l[(gc * 4 + 2) * 8 + m] = v.z;
-            sx_l[(gc * 4 + 3) * 8 + m] = v.w;
-        }
-        constexpr int U = 8;
-        const int nx = gcount * 8;
-        for (int c0 = threadIdx.x; c0 < nx; c0 += kThreads * U) {
-            uint4 v[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int c = c0 + u * kThreads;
-                const int g = c >> 3, m = c & 7;
-                v[u] = (c < nx && m < M)
-                           ? *reinterpret_cast<const uint4*>(xq + (size_t)m * K2 + (size_t)(g_begin + g) * 16)
-                           : make_uint4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int c = c0 + u * kThreads;
-                if (c < nx) {
-                    const int g = c >> 3, m = c & 7;
-                    *reinterpret_cast<uint2*>(x_l + (size_t)g * 128 + m * 8) = make_uint2(v[u].x, v[u].y);
-                    *reinterpret_cast<uint2*>(x_l + (size_t)g * 128 + 64 + m * 8) = make_uint2(v[u].z, v[u].w);
-                }
-            }
-        }
-        if (threadIdx.x < kStream8ZeroBytes / 16)
-            reinterpret_cast<uint4*>(x_zero)[threadIdx.x] = make_uint4(0, 0, 0, 0);
-    }
-    __syncthreads();
-    if (nb0 * kRows >= N) return;
-
-    // Activation operand: lane (r16 = m + 8e, q) reads half q%2 of group 2p+e
-    // of row m when q/2 == e, else a zero word.  Per stage the data lanes
-    // advance 8 groups (1024 B) and the zero lanes stay on the zero words.
-    const int am = r16 & 7, ae = r16 >> 3;
-    const bool a_data = (q >> 1) == ae;
-    const uint8_t* x_base = a_data ? x_l + ae * 128 + (q & 1) * 64 + am * 8 : x_zero;
-    const int x_step = a_data ? kStreamSG * 128 : 0;
-    const uint32_t sx_mask = ae ? 0xffff0000u : 0x0000ffffu;
-    const uint8_t* b_base = slab + q * kPlane + r16 * 8;
-
-    float acc[NH][4];
-#pragma unroll
-    for (int h = 0; h < NH; ++h)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[h][j] = 0.0f;
-
-    auto process = [&](int st, Stage& S) {
-        // 1. transpose this stage's weights into the slab, [group][half][row][8 B]
-#pragma unroll
-        for (int j = 0; j < kNW; ++j) {
-            const uint4 v = S.w[j];
-            const int row = 8 * j + (lane >> 3), g = lane & 7;
-            uint8_t* base = slab + row * 8;
-            *reinterpret_cast<uint2*>(base + (g * 2 + 0) * kPlane) = make_uint2(v.x, v.y);
-            *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kPlane) = make_uint2(v.z, v.w);
-        }
-        // 2. per group pair p: one activation operand, two 16-column halves,
-        //    software pipelined (pair p+1's MFMAs before pair p's fold)
-        const uint8_t* xa = x_base + (size_t)st * x_step;
-        auto issue = [&](int p, v4i (&d)[NH], v4f (&sc)[NH]) {
-            const uint2 xw = *reinterpret_cast<const uint2*>(xa + p * 256);
-            uint32_t a0, a1, a2, a3;
-            unpack_s4x8_x16(xw.x, a0, a1);
-            unpack_s4x8_x16(xw.y, a2, a3);
-            const v4i A = {(int)a0, (int)a1, (int)a2, (int)a3};
-            const uint32_t sxa = sx_l[(st * 4 + p) * 8 + am] & sx_mask;
-            const uint2 sa2 = (p & 1) ? make_uint2(0u, sxa) : make_uint2(sxa, 0u);
-#pragma unroll
-            for (int h = 0; h < NH; ++h) {
-                const uint2 w = *reinterpret_cast<const uint2*>(b_base + p * 4 * kPlane + h * 128);
-                uint32_t b0, b1, b2, b3;
-                unpack_s4x8_x16(w.x, b0, b1);
-                unpack_s4x8_x16(w.y, b2, b3);
-                const v4i B = {(int)b0, (int)b1, (int)b2, (int)b3};
-                const uint2 sb2 = (p < 2) ? make_uint2(S.sw[h].x, S.sw[h].y) : make_uint2(S.sw[h].z, S.sw[h].w);
-                d[h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, (v4i){0, 0, 0, 0}, 0, 0, 0);
-                sc[h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s, sa2),
-                                                                   __builtin_bit_cast(v4s, sb2),
-                                                                   (v4f){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-            }
-        };
-        auto fold = [&](const v4i (&d)[NH], const v4f (&sc)[NH]) {
-#pragma unroll
-            for (int h = 0; h < NH; ++h)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[h][j] = __builtin_fmaf((float)d[h][j], sc[h][j], acc[h][j]);
-        };
-        v4i d0[NH], d1[NH];
-        v4f s0[NH], s1[NH];
-        issue(0, d0, s0);
-        issue(1, d1, s1);
-        fold(d0, s0);
-        issue(2, d0, s0);
-        fold(d1, s1);
-        issue(3, d1, s1);
-        fold(d0, s0);
-        fold(d1, s1);
-    };
-
-    int st = 0;
-    for (; st + PF <= nst; st += PF) {
-#pragma unroll
-        for (int d = 0; d < PF; ++d) {
-            process(st + d, buf[d]);
-            load(min(st + d + PF, nst - 1), buf[d]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-#pragma unroll
-    for (int d = 0; d < PF - 1; ++d)
-        if (st + d < nst) process(st + d, buf[d]);
-
-    // even-group sums (lanes 0-31) + odd-group sums (lanes 32-63); lanes 0-31
-    // then hold rows m = 4q + j of columns 16h + r16
-#pragma unroll
-    for (int h = 0; h < NH; ++h) {
-        const int col = nb0 * kRows + 16 * h + r16;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float v = (acc[h][j] + __shfl_xor(acc[h][j], 32)) * kFold8OutScale;
-            const int row = 4 * q + j;
-            if (lane < 32 && row < M && col < N) {
-                if (partial != nullptr)
-                    partial[((size_t)blockIdx.y * M + row) * N + col] = v;
-                else
-                    y[(size_t)row * N + col] = f32_to_f16_bits(v);
-            }
-        }
-    }
-}
-
 // Sum the split-K partials in slice order and convert to fp16.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial,
                                                             uint16_t* __restrict__ y, int64_t MN,
@@ -862,42 +632,13 @@ __global__ void mfma_selftest_kernel(const int8_t* __restrict__ a, const int8_t*
 
 // ---------------------------------------------------------------- planning
 struct Plan {
-    int cfg;        // 0: 32x128 (M <= 32), 1: 64x128, 2: 128x128, 3: streaming (M <= 8),
-                    // 4: streaming with in-workgroup K split (8 < M <= 32)
+    int cfg;        // 0: 32x128 (M <= 32), 1: 64x128, 2: 128x128,
+                    // 4: streaming with in-workgroup K split (M <= 64)
     int mr;         // fold rows per 32-row block (cfg 0, 4)
     int splits;
     int groups_per_split;
     int tm, tn, sg;
 };
-
-#ifndef WUSH_STREAM_WAVES
-#define WUSH_STREAM_WAVES 1024   // M <= 8: split K until this many wavefronts stream (measured best)
-#endif
-#ifndef WUSH_STREAM_PFX
-#define WUSH_STREAM_PFX 2
-#endif
-constexpr int kStreamPFX = WUSH_STREAM_PFX;      // stages in flight per wavefront, M <= 8 kernel
-constexpr size_t kStreamLdsMax = 64 * 1024;
-
-// LDS bytes of an M <= 8 streaming launch with gps groups per slice: the
-// staged x scales (4 B per group pair and row) and codes (128 B per group),
-// the zero words, and the slabs.
-// Geometry of the M <= 8 kernel: 16 weight rows per wavefront (twice the
-// wavefronts of 32-row ones, which keeps more HBM requests in flight) and 8
-// wavefronts per workgroup sharing the staged activations.  Measured at L70:
-// 55.7 us (16 rows, 8 waves), 58.2 (32 rows, 4 waves), 63.0 (16 rows, 4
-// waves: 3 workgroups per CU do not hold 14 wavefronts); at Q8 it also beats
-// split-K (14.6 vs 18.7 us at M=1).
-#ifndef WUSH_S8_NH
-#define WUSH_S8_NH 1             // 16-column halves per wavefront of the M <= 8 kernel
-#endif
-#ifndef WUSH_S8_WPB
-#define WUSH_S8_WPB 8            // its wavefronts per workgroup
-#endif
-constexpr int kS8Rows = 16 * WUSH_S8_NH;
-static size_t stream8_smem(int64_t gps) {
-    return (size_t)gps * (16 + 128) + kStream8ZeroBytes + (size_t)WUSH_S8_WPB * kStreamSG * 2 * (kS8Rows * 8 + 16);
-}
 
 #ifndef WUSH_PF_BM
 #define WUSH_PF_BM 2             // prefill tile: 32x32 blocks per wavefront along M
@@ -961,7 +702,7 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
     Plan p;
     p.mr = 32;
     const int64_t G0 = K / 32;
-    if (allow_split && scales16 && M > 8 && M <= kStream32MaxM && K % 256 == 0) {
+    if (allow_split && scales16 && M <= kStream32MaxM && K % 256 == 0) {
         // in-workgroup K split: one workgroup of stream32_kw wavefronts per
         // 32-row block; split K across workgroups only while fewer than
         // kStream32Waves wavefronts would stream and every wavefront keeps
@@ -983,30 +724,6 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         p.splits = s;
         p.groups_per_split = (int)gps;
         return p;
-    }
-    if (allow_split && scales16 && M <= 8 && K % 256 == 0) {
-        // M <= 8 streaming kernel: one wavefront per kS8Rows weight rows
-        p.cfg = 3; p.tm = 32; p.sg = kStreamSG;
-        p.mr = 8;
-        p.tn = WUSH_S8_WPB * kS8Rows;
-        const int64_t waves = (N + kS8Rows - 1) / kS8Rows;
-        int s = 1;
-        while (s < 16 && waves * s < WUSH_STREAM_WAVES && G0 / (2 * s) >= 4 * kStreamSG) s *= 2;
-        int64_t gps = (G0 + s - 1) / s;
-        gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
-        while (stream8_smem(gps) > kStreamLdsMax && gps > kStreamSG) {
-            s *= 2;
-            gps = (G0 + s - 1) / s;
-            gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
-        }
-        s = (int)((G0 + gps - 1) / gps);
-        const bool ws_ok = s == 1 || (size_t)s * (size_t)M * (size_t)N * sizeof(float) <= ws_bytes_available;
-        if (ws_ok && stream8_smem(gps) <= kStreamLdsMax) {
-            p.splits = s;
-            p.groups_per_split = (int)gps;
-            return p;
-        }
-        p.mr = 32;
     }
     if (M <= 32) {
         p.cfg = 0; p.tm = 32; p.tn = 128; p.sg = 8;
@@ -1061,6 +778,13 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
         if constexpr (!PT) {
             dim3 grid((unsigned)((N + 31) / 32), (unsigned)p.splits);
             switch (p.mr) {
+                case 8: {
+                    constexpr int KW = stream32_kw(8);
+                    gemm_s4_stream32_kernel<8, 1, KW, WUSH_S32_PF16, WUSH_S32_OCC16>
+                        <<<grid, 64 * KW, stream32_smem(KW, 4), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
+                                                                         p.groups_per_split);
+                    break;
+                }
                 case 16: {
                     constexpr int KW = stream32_kw(16);
                     gemm_s4_stream32_kernel<16, 1, KW, WUSH_S32_PF16, WUSH_S32_OCC16>
@@ -1096,13 +820,6 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
                     }
                     break;
             }
-        }
-    } else if (p.cfg == 3) {
-        if constexpr (!PT) {
-            const size_t smem = stream8_smem(p.groups_per_split);
-            dim3 grid((unsigned)((N + p.tn - 1) / p.tn), (unsigned)p.splits);
-            gemm_s4_stream8_kernel<kStreamPFX, WUSH_S8_NH, WUSH_S8_WPB><<<grid, 64 * WUSH_S8_WPB, smem, stream>>>(
-                xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
         }
     } else if (p.cfg == 0) {
         if (PT || p.mr == 32)
