@@ -29,8 +29,11 @@ namespace wush {
 #ifndef WUSH_GEMV_WAVES_M
 #define WUSH_GEMV_WAVES_M 16    // ... for M >= 2: the staged activations (M*K*3/4 bytes of
 #endif                          // LDS) are shared by 16 wavefronts (L70 M=8: 51.5 vs 53.5 us)
+#ifndef WUSH_GEMV_WAVES_M78
+#define WUSH_GEMV_WAVES_M78 WUSH_GEMV_WAVES_M  // ... for M = 7, 8 (8 or 4 were slower with 1 row)
+#endif
 template <int M>
-constexpr int gemv_waves() { return M == 1 ? WUSH_GEMV_WAVES : WUSH_GEMV_WAVES_M; }
+constexpr int gemv_waves() { return M == 1 ? WUSH_GEMV_WAVES : M >= 7 ? WUSH_GEMV_WAVES_M78 : WUSH_GEMV_WAVES_M; }
 #ifndef WUSH_GEMV_RS
 #define WUSH_GEMV_RS 1          // recursive-halving reduction of the R x M outputs
 #endif
@@ -47,7 +50,10 @@ constexpr int gemv_waves() { return M == 1 ? WUSH_GEMV_WAVES : WUSH_GEMV_WAVES_M
 #define WUSH_GEMV_R4 2          // ... at M = 3, 4
 #endif
 #ifndef WUSH_GEMV_R8
-#define WUSH_GEMV_R8 2          // ... at M = 5 .. 8
+#define WUSH_GEMV_R8 2          // ... at M = 5, 6
+#endif
+#ifndef WUSH_GEMV_R78
+#define WUSH_GEMV_R78 1         // ... at M = 7, 8 (L70 M=8: 48.3 us with 1 row, 51.4 with 2)
 #endif
 
 __device__ __forceinline__ int dot32_s4(const uint4& a, const uint4& b, int init = 0) {
@@ -340,8 +346,8 @@ extern "C" int wush_gemv_int4(const uint8_t* xq, const uint16_t* xs, const uint8
         case 4: wush::launch_gemv<4, WUSH_GEMV_R4>(xq, xs, wq, ws, y, n, k, stream); break;
         case 5: wush::launch_gemv<5, WUSH_GEMV_R8>(xq, xs, wq, ws, y, n, k, stream); break;
         case 6: wush::launch_gemv<6, WUSH_GEMV_R8>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 7: wush::launch_gemv<7, WUSH_GEMV_R8>(xq, xs, wq, ws, y, n, k, stream); break;
-        default: wush::launch_gemv<8, WUSH_GEMV_R8>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 7: wush::launch_gemv<7, WUSH_GEMV_R78>(xq, xs, wq, ws, y, n, k, stream); break;
+        default: wush::launch_gemv<8, WUSH_GEMV_R78>(xq, xs, wq, ws, y, n, k, stream); break;
     }
     return (int)hipGetLastError();
 }
