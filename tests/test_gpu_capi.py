@@ -377,6 +377,39 @@ def test_gemm_stream_k_split_shapes(capi, M, N, K):
     assert rel_fro(y, ref) < FRO_TOL, (M, N, K, rel_fro(y, ref))
 
 
+def test_gemm_random_shapes_all_paths(capi):
+    # Seeded random shapes over every planner branch: the streaming kernel
+    # (K % 256 == 0, M <= 64, with and without split-K), the LDS tiles (other
+    # K, M > 64), ragged N, and 2-byte-aligned scales (the tiles at any M);
+    # the GEMV beside them at M <= 8.  Each against the fp64 oracle product.
+    import torch
+    g = rng(4400)
+    for case in range(24):
+        M = int(g.choice([1, 2, 3, 5, 8, 9, 16, 23, 31, 32, 33, 47, 64, 65, 100, 200]))
+        N = int(g.integers(1, 3000))
+        K = 32 * int(g.choice([1, 3, 8, 9, 16, 24, 40, 64, 96, 128]))
+        xq, xs, wq, ws = _rand_operands(g, M, N, K)
+        ref = oracle.gemm_f64(xq, xs, wq, ws)
+        y = run_gemm(capi, xq, xs, wq, ws)
+        assert rel_fro(y, ref) < FRO_TOL, (case, M, N, K, rel_fro(y, ref))
+        if M <= 8 and M * K * 3 // 4 <= 65536:
+            y2 = run_gemm(capi, xq, xs, wq, ws, "gemv")
+            assert rel_fro(y2, ref) < FRO_TOL, (case, M, N, K, "gemv")
+        # 2-byte-aligned scales take the tiles whatever M and K are
+        dx, dw = to_dev_u8(xq), to_dev_u8(wq)
+        bx = torch.zeros(xs.size + 8, dtype=torch.bfloat16, device="cuda")
+        bw = torch.zeros(ws.size + 8, dtype=torch.bfloat16, device="cuda")
+        bx[1:1 + xs.size] = to_dev_bf16(xs).reshape(-1)
+        bw[1:1 + ws.size] = to_dev_bf16(ws).reshape(-1)
+        y3 = torch.empty(M, N, dtype=torch.float16, device="cuda")
+        wsb = capi.gemm_s4_workspace_bytes(M, N, K)
+        work = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+        capi.gemm_s4(dx.data_ptr(), bx.data_ptr() + 2, dw.data_ptr(), bw.data_ptr() + 2, y3.data_ptr(),
+                     M, N, K, work.data_ptr() if wsb else None, wsb, _stream())
+        torch.cuda.synchronize()
+        assert rel_fro(f16_tensor_f64(y3), ref) < FRO_TOL, (case, M, N, K, "unaligned scales")
+
+
 def test_gemm_golden_fixture(capi):
     gm = np.load(os.path.join(GOLDEN, "gemm_small.npz"))
     y = run_gemm(capi, gm["xq"], gm["xs"], gm["wq"], gm["ws"])
