@@ -643,6 +643,10 @@ struct Plan {
 #ifndef WUSH_PF_BM
 #define WUSH_PF_BM 2             // prefill tile: 32x32 blocks per wavefront along M
 #endif
+#ifndef WUSH_PF_MIN_TILES
+#define WUSH_PF_MIN_TILES 400    // fewer 128x128 tiles than this take 64x128 tiles (plus split-K):
+#endif                           // M=128 K=N=8192 55.4 -> 46.5 us, M=256 K=4096 N=24576 (384 tiles)
+                                 // 101.5 -> 96.0 us; L70 M=128 (448 tiles) 216 us with 128x128, 230 without
 #ifndef WUSH_PF_BN
 #define WUSH_PF_BN 2             // and along N (2 x 2 wavefronts per workgroup)
 #endif
@@ -725,10 +729,12 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         p.groups_per_split = (int)gps;
         return p;
     }
+    const int64_t big_tiles = ((M + 32 * WUSH_PF_BM * 2 - 1) / (32 * WUSH_PF_BM * 2)) *
+                              ((N + 32 * WUSH_PF_BN * 2 - 1) / (32 * WUSH_PF_BN * 2));
     if (M <= 32) {
         p.cfg = 0; p.tm = 32; p.tn = 128; p.sg = 8;
         p.mr = (int)((M + 7) / 8 * 8);
-    } else if (M <= 64) {
+    } else if (M <= 64 || big_tiles < WUSH_PF_MIN_TILES) {
         p.cfg = 1; p.tm = 64; p.tn = 128; p.sg = 8;
     } else {
         p.cfg = 2; p.tm = 32 * WUSH_PF_BM * 2; p.tn = 32 * WUSH_PF_BN * 2; p.sg = 4;
