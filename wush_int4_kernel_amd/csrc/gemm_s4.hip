@@ -675,6 +675,10 @@ struct Plan {
 #ifndef WUSH_S32_OCC32
 #define WUSH_S32_OCC32 4         // (128 VGPRs either way with the 2-deep group pipeline)
 #endif
+#ifndef WUSH_S32_MIN_STAGES
+#define WUSH_S32_MIN_STAGES 2    // split K across workgroups only while every wavefront keeps this many stages
+                                 // (1 was slower at M <= 16 and equal elsewhere: the split-K sum costs more)
+#endif
 #ifndef WUSH_S32_WAVES
 #define WUSH_S32_WAVES 2048      // split K across workgroups below this many wavefronts
 #endif
@@ -716,7 +720,8 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         const int kw = stream32_kw(p.mr, N);
         const int64_t wgs = (N + 31) / 32;
         int s = 1;
-        while (s < 16 && wgs * s * kw < kStream32Waves && G0 / (2 * s) >= (int64_t)kw * 2 * kStreamSG)
+        while (s < 16 && wgs * s * kw < kStream32Waves &&
+               G0 / (2 * s) >= (int64_t)kw * WUSH_S32_MIN_STAGES * kStreamSG)
             s *= 2;
         int64_t gps = (G0 + s - 1) / s;
         gps = (gps + kStreamSG - 1) / kStreamSG * kStreamSG;
