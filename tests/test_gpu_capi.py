@@ -410,6 +410,124 @@ def test_gemm_random_shapes_all_paths(capi):
         assert rel_fro(f16_tensor_f64(y3), ref) < FRO_TOL, (case, M, N, K, "unaligned scales")
 
 
+# Shapes the planner sends to the 256x256 fp16-MFMA tiles (K % 256 == 0,
+# M >= 512, at least 256 tiles): ragged M and N, one and several load batches.
+H16_SHAPES = [(512, 32768, 256), (700, 30000, 512), (1030, 16400, 1024), (4096, 4096, 2048)]
+
+
+def _sample(g, n, k):
+    """k sorted indices of range(n), always holding the first and the last."""
+    idx = set(g.choice(n, size=min(n, k), replace=False).tolist()) | {0, n - 1}
+    return np.array(sorted(idx))
+
+
+def _run_gemm_unaligned(capi, xq, xs, wq, ws):
+    """wush_gemm_s4 with both scale tensors at 2-byte (not 16-byte) alignment."""
+    import torch
+    M, N, K = xq.shape[0], wq.shape[0], 2 * xq.shape[1]
+    dx, dw = to_dev_u8(xq), to_dev_u8(wq)
+    bx = torch.zeros(xs.size + 8, dtype=torch.bfloat16, device="cuda")
+    bw = torch.zeros(ws.size + 8, dtype=torch.bfloat16, device="cuda")
+    bx[1:1 + xs.size] = to_dev_bf16(xs).reshape(-1)
+    bw[1:1 + ws.size] = to_dev_bf16(ws).reshape(-1)
+    y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    assert capi.gemm_s4_workspace_bytes(M, N, K) == 0
+    capi.gemm_s4(dx.data_ptr(), bx.data_ptr() + 2, dw.data_ptr(), bw.data_ptr() + 2, y.data_ptr(),
+                 M, N, K, None, 0, _stream())
+    torch.cuda.synchronize()
+    return f16_tensor_f64(y)
+
+
+@pytest.mark.parametrize("M,N,K", H16_SHAPES)
+def test_gemm_h16_matches_oracle(capi, M, N, K):
+    # fp16 operands code*scale (exact) with fp32 accumulation over the whole
+    # K: seeded samples of rows and columns (first and last always) against
+    # the fp64 oracle, for 16-byte and 2-byte aligned scales
+    g = rng(4500 + M + N + K)
+    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    rows, cols = _sample(g, M, 40), _sample(g, N, 1500)
+    ref = oracle.gemm_f64(xq[rows], xs[rows], wq[cols], ws[cols])
+    for name, y in (("aligned", run_gemm(capi, xq, xs, wq, ws)),
+                    ("unaligned", _run_gemm_unaligned(capi, xq, xs, wq, ws))):
+        got = y[np.ix_(rows, cols)]
+        assert rel_fro(got, ref) < FRO_TOL, (M, N, K, name, rel_fro(got, ref))
+        assert np.abs(got - ref).max() < 0.05 * max(1.0, np.abs(ref).max())
+        assert np.isfinite(y).all()
+
+
+def test_gemm_h16_int_exact_and_group_dots(capi):
+    # unit scales and small codes: integer sums, exact in fp16; then scales 1
+    # on one group only and 0 elsewhere: y = D[:, :, g] exactly
+    g = rng(4510)
+    M, N, K = 512, 32768, 256
+    xq = pack_codes(g.integers(-2, 3, (M, K)))
+    wq = pack_codes(g.integers(-2, 3, (N, K)))
+    xs = np.full((M, K // 32), 0x3F80, np.uint16)
+    ws = np.full((N, K // 32), 0x3F80, np.uint16)
+    rows, cols = _sample(g, M, 64), _sample(g, N, 2048)
+    y = run_gemm(capi, xq, xs, wq, ws)
+    D = oracle.group_dots(xq[rows], wq[cols]).astype(np.float64)
+    assert np.array_equal(y[np.ix_(rows, cols)], D.sum(axis=2))
+    xq, _, wq, _ = _rand_operands(g, M, N, K)
+    D = oracle.group_dots(xq[rows], wq[cols]).astype(np.float64)
+    for gg in range(K // 32):
+        xs = np.zeros((M, K // 32), np.uint16)
+        ws = np.zeros((N, K // 32), np.uint16)
+        xs[:, gg] = 0x3F80
+        ws[:, gg] = 0x3F80
+        y = run_gemm(capi, xq, xs, wq, ws)
+        assert np.array_equal(y[np.ix_(rows, cols)], D[:, :, gg]), gg
+
+
+def _bf16_times_pow2(bits, e):
+    """bf16 bits of positive normal values times 2^e (e broadcast), exactly."""
+    b = bits.astype(np.int64) + (np.asarray(e, np.int64) << 7)
+    assert ((b >> 7) > 0).all() and ((b >> 7) < 255).all()
+    return b.astype(np.uint16)
+
+
+def test_gemm_h16_scale_range(capi):
+    # Scales far outside fp16's range (activation rows near 2^+40, weight
+    # columns near 2^-40, and a spread of 2^-12..2^+12 across the groups of a
+    # row) so that every row and column needs its own power-of-two shift; the
+    # products stay in fp16 range.  Compared with the oracle after removing
+    # each row's and column's factor.
+    g = rng(4520)
+    M, N, K = 600, 24000, 1024
+    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    dr = g.integers(-3, 2, M)                    # outputs |y| < 2^11 * 2^2 stay finite in fp16
+    dc = g.integers(-3, 2, N)
+    spread = g.integers(-12, 13, (M, K // 32))
+    xs2 = _bf16_times_pow2(xs, 40 + dr[:, None] + spread)
+    ws2 = _bf16_times_pow2(ws, -40 + dc[:, None])
+    rows, cols = _sample(g, M, 40), _sample(g, N, 1500)
+    xs_ref = _bf16_times_pow2(xs, spread)[rows]
+    ref = oracle.gemm_f64(xq[rows], xs_ref, wq[cols], ws[cols])
+    y = run_gemm(capi, xq, xs2, wq, ws2)[np.ix_(rows, cols)]
+    got = y * np.ldexp(1.0, -(dr[rows][:, None] + dc[cols][None, :]))
+    assert rel_fro(got, ref) < FRO_TOL, rel_fro(got, ref)
+
+
+def test_gemm_h16_nonfinite_scales(capi):
+    # a non-finite activation scale makes its row NaN, a non-finite weight
+    # scale its column, as in the dequantized product; the rest is unaffected
+    g = rng(4530)
+    M, N, K = 512, 32768, 512
+    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    xs[3, 2] = 0x7F80                            # +inf
+    xs[300, 15] = 0xFFC0                         # NaN
+    ws[5, 1] = 0x7FC0                            # NaN
+    ws[20000, 9] = 0xFF80                        # -inf
+    y = run_gemm(capi, xq, xs, wq, ws)
+    bad_r, bad_c = [3, 300], [5, 20000]
+    assert np.isnan(y[bad_r]).all() and np.isnan(y[:, bad_c]).all()
+    rows = np.array([r for r in _sample(g, M, 40) if r not in bad_r])
+    cols = np.array([c for c in _sample(g, N, 1500) if c not in bad_c])
+    ref = oracle.gemm_f64(xq[rows], xs[rows], wq[cols], ws[cols])
+    got = y[np.ix_(rows, cols)]
+    assert rel_fro(got, ref) < FRO_TOL, rel_fro(got, ref)
+
+
 def test_gemm_golden_fixture(capi):
     gm = np.load(os.path.join(GOLDEN, "gemm_small.npz"))
     y = run_gemm(capi, gm["xq"], gm["xs"], gm["wq"], gm["ws"])

@@ -25,7 +25,7 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libwush_int4.so")
 EXT = os.path.join(PKG, "_C" + sysconfig.get_config_var("EXT_SUFFIX"))
 
-HIP_SOURCES = ["quant.hip", "fused_tq.hip", "gemv.hip", "gemm_s4.hip"]
+HIP_SOURCES = ["quant.hip", "fused_tq.hip", "gemv.hip", "gemm_s4.hip", "gemm_h16.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -38,12 +38,19 @@ HIPCC_FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA results in VGPRs: the fold reads every accumulator element, and an
-    # AGPR destination would add one v_accvgpr_read per element
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-command-line-argument",
 ]
+
+# MFMA results in VGPRs: the int8 kernels' fold reads every accumulator
+# element, and an AGPR destination would add one v_accvgpr_read per element.
+# gemm_h16.hip keeps its 256 accumulators per wavefront in AGPRs instead.
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+AGPR_SOURCES = {"gemm_h16.hip"}
+
+
+def source_flags(src: str) -> list:
+    return HIPCC_FLAGS + ([] if src in AGPR_SOURCES else VGPR_FORM)
 
 
 def _run(cmd, verbose):
@@ -68,10 +75,10 @@ def build_capi(verbose: bool = False) -> str:
 
     def compile_one(src):
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-        _run([cc, *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj], verbose)
+        _run([cc, *source_flags(src), f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj], verbose)
         return obj
 
-    with cf.ThreadPoolExecutor(max_workers=min(4, len(HIP_SOURCES))) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(5, len(HIP_SOURCES))) as ex:
         objs = list(ex.map(compile_one, HIP_SOURCES))
     tmp = LIB + ".tmp"
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)

@@ -1,0 +1,21 @@
+// gemm_h16.h -- launcher of the fp16-MFMA prefill GEMM (gemm_h16.hip), called
+// by the planner in gemm_s4.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace wush {
+
+// LDS bytes of one workgroup (the launcher raises the kernel's dynamic LDS
+// limit to this once).
+size_t gemm_h16_smem_bytes();
+
+// y = group-scaled product, M x N fp16, for M, N >= 1 and K % 256 == 0 (code
+// tensors 16-byte aligned, scales 2-byte aligned); hipErrorInvalidValue
+// otherwise.
+int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
+                    uint16_t* y, int M, int N, int K, hipStream_t stream);
+
+}  // namespace wush

@@ -1,0 +1,416 @@
+// gemm_h16.hip -- group-scaled W4A4 GEMM for prefill-sized M on fp16 MFMA
+// (csrc/gemm_s4.cu:85-379 is the reference contract).
+//
+//   y[m][n] = sum_g sum_{k in g} (qx[m][k] * sx[m][g]) * (qw[n][k] * sw[n][g])
+//
+// The int8 kernels fold every 32x32 block of exact group dots into fp32 with
+// two VALU operations per output and group, which bounds them at a quarter of
+// the int8 MFMA rate.  Here the scales go into the operands instead: a code
+// (3 bits of magnitude) times a bf16 scale (8-bit significand) is exact in
+// fp16 (11-bit significand) once the scale sits in fp16's exponent range, and
+// the product of two such operands is exact in fp32 (22 bits).  So
+// v_mfma_f32_32x32x16_f16 accumulates exact terms in fp32 over the whole K and
+// nothing runs per output in the main loop.
+//
+// Range: every activation row m gets a power of two 2^ea[m], chosen from the
+// row's largest scale so that it lands in [2^12, 2^13) (code * scale <= 7 *
+// 2^13 < 65504); likewise 2^eb[n] per weight column.  The epilogue multiplies
+// by 2^-(ea[m] + eb[n]) with v_ldexp_f32 (exact).  Every scale down to
+// 2^-22 of its row's largest converts exactly; smaller ones land in fp16's
+// subnormal range and keep fewer bits (an absolute error below 2^-36 of the
+// row's largest scale per term).  A row or column with a non-finite scale
+// gives NaN, as the reference's dequantized product does (code 0 * inf).
+//
+// Workgroup: 4 wavefronts in 2 x 2, a 256 x 256 output tile, each wavefront
+// 128 x 128 (16 accumulator blocks, 256 AGPRs), one workgroup per CU.  A stage
+// is one group (K = 32): thread t converts row t of the activation tile and
+// column t of the weight tile (16 code bytes each) to fp16 in a
+// double-buffered LDS tile laid out fragment-major, [K16 slice][32-row block]
+// [k-half][row][8 halves], so that a wavefront's operand read of one 32-row
+// block is 1 KiB contiguous (lane l at 16*l) and the conversion writes of
+// 64 consecutive rows are contiguous too.  Global loads run in batches of four
+// groups (64 bytes of every row, four stages ahead), four lanes per row so an
+// instruction reads 16 rows of 64 contiguous bytes, then a 4 x 4 in-quad
+// transpose gives every lane its own row; addresses are clamped, so the loop
+// has no conditional loads.
+#include "wush_device.h"
+#include "gemm_h16.h"
+
+namespace wush {
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kH16Tile = 256;                    // output rows and columns per workgroup
+constexpr int kH16Slice = kH16Tile * 32;         // bytes of one K16 slice of one operand (256 rows x 16 halves)
+constexpr int kH16Op = 2 * kH16Slice;            // one group of one operand
+constexpr int kH16Buf = 2 * kH16Op;              // activations + weights of one group
+constexpr int kH16Batch = 4;                     // groups per global load batch
+constexpr int kH16NonFinite = 1 << 20;           // row/column shift marking a non-finite scale
+
+// Power of two that moves the largest |scale| of a row (bf16 bits mx, sign
+// cleared) into [2^12, 2^13): mx < 2^(e-126) for exponent field e.
+__device__ __forceinline__ int h16_shift(uint32_t mx) {
+    return mx >= 0x7f80u ? kH16NonFinite : 139 - (int)(mx >> 7);
+}
+
+// Largest |bf16| of the n scales of an activation row (pa) and of a weight
+// column (pb), as bits with the sign cleared.  Loads go out 8 per row per
+// round trip: one at a time, the 2 * G / 8 dependent loads of a long row cost
+// a memory latency each.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ u16x2 abs_bits2(uint32_t w) {
+    return __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
+}
+
+template <bool VEC>
+__device__ __forceinline__ void h16_row_max(const uint16_t* __restrict__ pa, const uint16_t* __restrict__ pb,
+                                            int n, uint32_t& mxa, uint32_t& mxb) {
+    u16x2 ma = {0, 0}, mb = {0, 0};
+    if constexpr (VEC) {
+        const uint4* qa = reinterpret_cast<const uint4*>(pa);
+        const uint4* qb = reinterpret_cast<const uint4*>(pb);
+        const int n8 = n >> 3;
+        int i = 0;
+        for (; i + 8 <= n8; i += 8) {
+            uint4 va[8], vb[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                va[u] = qa[i + u];
+                vb[u] = qb[i + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                ma = __builtin_elementwise_max(ma, __builtin_elementwise_max(abs_bits2(va[u].x), abs_bits2(va[u].y)));
+                ma = __builtin_elementwise_max(ma, __builtin_elementwise_max(abs_bits2(va[u].z), abs_bits2(va[u].w)));
+                mb = __builtin_elementwise_max(mb, __builtin_elementwise_max(abs_bits2(vb[u].x), abs_bits2(vb[u].y)));
+                mb = __builtin_elementwise_max(mb, __builtin_elementwise_max(abs_bits2(vb[u].z), abs_bits2(vb[u].w)));
+            }
+        }
+        for (; i < n8; ++i) {
+            const uint4 va = qa[i], vb = qb[i];
+            ma = __builtin_elementwise_max(ma, __builtin_elementwise_max(abs_bits2(va.x), abs_bits2(va.y)));
+            ma = __builtin_elementwise_max(ma, __builtin_elementwise_max(abs_bits2(va.z), abs_bits2(va.w)));
+            mb = __builtin_elementwise_max(mb, __builtin_elementwise_max(abs_bits2(vb.x), abs_bits2(vb.y)));
+            mb = __builtin_elementwise_max(mb, __builtin_elementwise_max(abs_bits2(vb.z), abs_bits2(vb.w)));
+        }
+    } else {
+        int i = 0;
+        for (; i + 16 <= n; i += 16) {
+            uint32_t va[16], vb[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                va[u] = pa[i + u];
+                vb[u] = pb[i + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                ma = __builtin_elementwise_max(ma, abs_bits2(va[u]));
+                mb = __builtin_elementwise_max(mb, abs_bits2(vb[u]));
+            }
+        }
+        for (; i < n; ++i) {
+            ma = __builtin_elementwise_max(ma, abs_bits2(pa[i]));
+            mb = __builtin_elementwise_max(mb, abs_bits2(pb[i]));
+        }
+    }
+    mxa = max((uint32_t)ma.x, (uint32_t)ma.y);
+    mxb = max((uint32_t)mb.x, (uint32_t)mb.y);
+}
+
+// Scale operand pair (s, s) and (s/16, s/16) in fp16 for the fp32 value f
+// of a bf16 scale and the row's shift.
+__device__ __forceinline__ void h16_scale(float f, int shift, h2& s, h2& s16) {
+    const _Float16 a = (_Float16)__builtin_ldexpf(f, shift);
+    const _Float16 c = (_Float16)__builtin_ldexpf(f, shift - 4);
+    s = (h2){a, a};
+    s16 = (h2){c, c};
+}
+
+// 8 s4 codes (element 2k in the low nibble of byte k) -> 8 fp16 code*scale
+// values, in the order k = 0,4,1,5,2,6,3,7 (the same for both operands, so
+// the dot product only sums in another order).  After the XOR each nibble is
+// code + 8 in [1, 15]; OR-ing it into 0x6400 (1024.0) gives 1024 + code + 8
+// (low nibble) or 1024 + 16 * (code + 8) (high nibble of a byte), both exact;
+// the subtraction leaves code or 16 * code exactly and the product with s or
+// s/16 is one exact fp16 rounding.
+__device__ __forceinline__ uint4 h16_codes(uint32_t w, h2 s, h2 s16) {
+    const uint32_t t = w ^ 0x88888888u;
+    const uint32_t t8 = t >> 8;
+    const h2 b0 = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const h2 b1 = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2 p0 = __builtin_bit_cast(h2, (t & 0x000F000Fu) | 0x64006400u);
+    const h2 p1 = __builtin_bit_cast(h2, (t & 0x00F000F0u) | 0x64006400u);
+    const h2 p2 = __builtin_bit_cast(h2, (t8 & 0x000F000Fu) | 0x64006400u);
+    const h2 p3 = __builtin_bit_cast(h2, (t8 & 0x00F000F0u) | 0x64006400u);
+    uint4 r;
+    r.x = __builtin_bit_cast(uint32_t, (h2)((p0 - b0) * s));
+    r.y = __builtin_bit_cast(uint32_t, (h2)((p1 - b1) * s16));
+    r.z = __builtin_bit_cast(uint32_t, (h2)((p2 - b0) * s));
+    r.w = __builtin_bit_cast(uint32_t, (h2)((p3 - b1) * s16));
+    return r;
+}
+
+// One load batch of a thread: 4 groups of its activation row and weight
+// column.  Scales: with VEC, sa[0..1] / sb[0..1] hold the 4 bf16 scales as
+// two packed pairs (one 8-byte load per row); otherwise sa[i] / sb[i] hold
+// group i's bf16 bits.
+// Value of the partner lane's `other` (DPP quad permutation CTRL: 0xB1 =
+// [1,0,3,2], lane ^ 1; 0x4E = [2,3,0,1], lane ^ 2) where take_other, else keep.
+template <int CTRL>
+__device__ __forceinline__ uint32_t h16_xchg(uint32_t keep, uint32_t other, bool take_other) {
+    const uint32_t v = (uint32_t)__builtin_amdgcn_mov_dpp((int)other, CTRL, 0xf, 0xf, false);
+    return take_other ? v : keep;
+}
+
+struct H16Batch {
+    uint4 a[kH16Batch];
+    uint4 b[kH16Batch];
+    uint32_t sa[kH16Batch];
+    uint32_t sb[kH16Batch];
+};
+
+// fp32 value of scale i of a batch (bits are only re-read here, at the
+// conversion, so the load's wait lands there too)
+template <bool VEC>
+__device__ __forceinline__ float h16_batch_scale(const uint32_t (&v)[kH16Batch], int i) {
+    if constexpr (VEC) return __uint_as_float((i & 1) ? (v[i >> 1] & 0xffff0000u) : (v[i >> 1] << 16));
+    return __uint_as_float(v[i] << 16);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_h16_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restrict__ xs,
+                     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ ws,
+                     uint16_t* __restrict__ y, int M, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    int* sh_ea = reinterpret_cast<int*>(smem + 2 * kH16Buf);
+    int* sh_eb = sh_ea + kH16Tile;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int m0 = blockIdx.y * kH16Tile;
+    const int n0 = blockIdx.x * kH16Tile;
+    const int G = K >> 5;
+    const int K2 = K >> 1;
+
+    // this thread's activation row and weight column for the scales (clamped:
+    // rows past the end load valid data and are never stored)
+    const int ra = min(m0 + tid, M - 1);
+    const int rb = min(n0 + tid, N - 1);
+    const uint16_t* psa = xs + (size_t)ra * G;
+    const uint16_t* psb = ws + (size_t)rb * G;
+
+    // Code loads, coalesced: lane (q, p) = (lane / 4, lane % 4) reads 16
+    // bytes of group 4b + p of the wavefront's rows 4q + i (i = 0..3), so one
+    // load instruction covers 16 rows x 64 contiguous bytes.  Lane (q, p)
+    // then holds X[i] = (row 4q+i, group p); h16_transpose turns that into
+    // (row 4q+p = its own row, group i) at the batch's first conversion.
+    const int p4 = lane & 3;
+    const int wrow = m0 + wave * 64 + (lane & ~3);   // row of X[0] in the activation tile
+    const int wcol = n0 + wave * 64 + (lane & ~3);
+    const uint8_t* qa[kH16Batch];
+    const uint8_t* qb[kH16Batch];
+#pragma unroll
+    for (int i = 0; i < kH16Batch; ++i) {
+        qa[i] = xq + (size_t)min(wrow + i, M - 1) * K2 + p4 * 16;
+        qb[i] = wq + (size_t)min(wcol + i, N - 1) * K2 + p4 * 16;
+    }
+    auto load_batch = [&](int b, H16Batch& r) {
+        // G % 8 == 0: a batch never straddles the end of a row; the clamp
+        // keeps the loads of batches past the end inside the last one
+        const int g0 = min(b * kH16Batch, G - kH16Batch) * 16;
+#pragma unroll
+        for (int i = 0; i < kH16Batch; ++i) {
+            r.a[i] = *reinterpret_cast<const uint4*>(qa[i] + g0);
+            r.b[i] = *reinterpret_cast<const uint4*>(qb[i] + g0);
+        }
+        if constexpr (VEC) {
+            const int g = min(b * kH16Batch, G - kH16Batch);
+            const uint2 va = *reinterpret_cast<const uint2*>(psa + g);
+            const uint2 vb = *reinterpret_cast<const uint2*>(psb + g);
+            r.sa[0] = va.x; r.sa[1] = va.y;
+            r.sb[0] = vb.x; r.sb[1] = vb.y;
+        } else {
+#pragma unroll
+            for (int i = 0; i < kH16Batch; ++i) {
+                const int g = min(b * kH16Batch + i, G - 1);
+                r.sa[i] = psa[g];
+                r.sb[i] = psb[g];
+            }
+        }
+    };
+
+    // 4 x 4 transpose of the batch's code chunks across the lanes of a quad
+    // (butterflies over lane bit 0, then bit 1): afterwards a[i] / b[i] hold
+    // group i of this lane's own row / column.
+    const bool odd1 = (lane & 1) != 0;
+    const bool odd2 = (lane & 2) != 0;
+    auto transpose = [&](uint4 (&x)[kH16Batch]) {
+        uint4 z[kH16Batch];
+#pragma unroll
+        for (int i = 0; i < kH16Batch; ++i) {
+            const bool own = ((i & 1) != 0) == odd1;
+            const uint4 o = x[i ^ 1];
+            z[i].x = h16_xchg<0xB1>(x[i].x, o.x, !own);
+            z[i].y = h16_xchg<0xB1>(x[i].y, o.y, !own);
+            z[i].z = h16_xchg<0xB1>(x[i].z, o.z, !own);
+            z[i].w = h16_xchg<0xB1>(x[i].w, o.w, !own);
+        }
+#pragma unroll
+        for (int i = 0; i < kH16Batch; ++i) {
+            const bool own = ((i & 2) != 0) == odd2;
+            const uint4 o = z[i ^ 2];
+            x[i].x = h16_xchg<0x4E>(z[i].x, o.x, !own);
+            x[i].y = h16_xchg<0x4E>(z[i].y, o.y, !own);
+            x[i].z = h16_xchg<0x4E>(z[i].z, o.z, !own);
+            x[i].w = h16_xchg<0x4E>(z[i].w, o.w, !own);
+        }
+    };
+
+    // row shifts first: their loads are waited for here, so the batch loads
+    // below start the main loop's load pattern with nothing else in flight
+    uint32_t mxa, mxb;
+    h16_row_max<VEC>(psa, psb, G, mxa, mxb);
+    const int ea = h16_shift(mxa);
+    const int eb = h16_shift(mxb);
+    sh_ea[tid] = ea;
+    sh_eb[tid] = eb;
+
+    H16Batch R0, R1;
+    load_batch(0, R0);
+    load_batch(1, R1);
+
+    // conversion writes: row tid of each operand, u32 j of the group's 16
+    // code bytes -> K16 slice j/2, k-half j%2
+    const int wofs = (tid >> 5) * 1024 + (tid & 31) * 16;
+    auto convert = [&](int buf, H16Batch& r, int i) {
+        if (i == 0) {
+            transpose(r.a);
+            transpose(r.b);
+        }
+        uint8_t* base = smem + buf * kH16Buf;
+        h2 s, s16;
+        h16_scale(h16_batch_scale<VEC>(r.sa, i), ea, s, s16);
+        const uint32_t wa[4] = {r.a[i].x, r.a[i].y, r.a[i].z, r.a[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<uint4*>(base + (j >> 1) * kH16Slice + (j & 1) * 512 + wofs) = h16_codes(wa[j], s, s16);
+        h16_scale(h16_batch_scale<VEC>(r.sb, i), eb, s, s16);
+        const uint32_t wb[4] = {r.b[i].x, r.b[i].y, r.b[i].z, r.b[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<uint4*>(base + kH16Op + (j >> 1) * kH16Slice + (j & 1) * 512 + wofs) =
+                h16_codes(wb[j], s, s16);
+    };
+
+    v16f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (v16f){0.0f};
+
+    const int rba = (wave >> 1) * 4;             // first 32-row block of this wavefront's activations
+    const int rbb = (wave & 1) * 4;              // ... and weight columns
+    auto compute = [&](int buf) {
+        const uint8_t* base = smem + buf * kH16Buf;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            h8 af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                af[i] = *reinterpret_cast<const h8*>(base + kk * kH16Slice + (rba + i) * 1024 + lane * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                bf[i] = *reinterpret_cast<const h8*>(base + kH16Op + kk * kH16Slice + (rbb + i) * 1024 + lane * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    convert(0, R0, 0);
+    __syncthreads();
+
+    // Stage s computes group s from buffer s&1 and converts group s+1 into
+    // the other buffer; batch b's registers are reloaded with batch b+2 right
+    // after their last group is converted.  G % 8 == 0, so the loop has one
+    // exit (exits from inside the unrolled body make the register allocator
+    // spill the batch registers); the last stage converts a clamped copy of
+    // group G-1 that is never computed.
+    for (int s0 = 0; s0 < G; s0 += 2 * kH16Batch) {
+#pragma unroll
+        for (int j = 0; j < 2 * kH16Batch; ++j) {
+            compute(j & 1);
+            if (j < kH16Batch - 1) convert((j + 1) & 1, R0, j + 1);
+            else if (j == kH16Batch - 1) convert(0, R1, 0);
+            else if (j < 2 * kH16Batch - 1) convert((j + 1) & 1, R1, j + 1 - kH16Batch);
+            else convert(0, R0, 0);
+            if (j == kH16Batch - 1) load_batch(s0 / kH16Batch + 2, R0);
+            if (j == 2 * kH16Batch - 1) load_batch(s0 / kH16Batch + 3, R1);
+            __syncthreads();
+            // keep each stage's work between its barriers: the scheduler
+            // would otherwise hoist the conversion of freshly loaded groups
+            // next to their loads and wait out the memory latency there
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // epilogue: y = acc * 2^-(ea + eb), NaN for a non-finite scale
+    const int half = lane >> 5;
+    const int l32 = lane & 31;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int cl = (rbb + j) * 32 + l32;
+        const int col = n0 + cl;
+        const int e_col = sh_eb[cl];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int rl = (rba + i) * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+                const int row = m0 + rl;
+                const int e_row = sh_ea[rl];
+                float v = __builtin_ldexpf(acc[i][j][e], -(e_row + e_col));
+                if (e_row == kH16NonFinite || e_col == kH16NonFinite) v = __builtin_nanf("");
+                if (row < M && col < N) y[(size_t)row * N + col] = f32_to_f16_bits(v);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+size_t gemm_h16_smem_bytes() { return 2 * kH16Buf + 2 * kH16Tile * sizeof(int); }
+
+int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
+                    uint16_t* y, int M, int N, int K, hipStream_t stream) {
+    const int G = K >> 5;
+    if (M <= 0 || N <= 0 || K <= 0 || K % 256 != 0) return (int)hipErrorInvalidValue;
+    const bool vec = G % 8 == 0 && ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws)) & 15u) == 0;
+    dim3 grid((unsigned)((N + kH16Tile - 1) / kH16Tile), (unsigned)((M + kH16Tile - 1) / kH16Tile));
+    const size_t smem = gemm_h16_smem_bytes();
+    static bool attr_set = false;                // above the default 64 KiB of dynamic LDS
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_h16_kernel<true>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_h16_kernel<false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e != hipSuccess) return (int)e;
+        attr_set = true;
+    }
+    if (vec)
+        gemm_h16_kernel<true><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, M, N, K);
+    else
+        gemm_h16_kernel<false><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, M, N, K);
+    return (int)hipGetLastError();
+}
+
+}  // namespace wush

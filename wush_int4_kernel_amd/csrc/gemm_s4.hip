@@ -25,6 +25,7 @@
 // a caller-provided workspace and a second kernel sums the slices in a fixed
 // order (deterministic, graph-capturable, no atomics, no memset).
 #include "wush_device.h"
+#include "gemm_h16.h"
 #include "../../include/wush_int4.h"
 
 namespace wush {
@@ -633,7 +634,8 @@ __global__ void mfma_selftest_kernel(const int8_t* __restrict__ a, const int8_t*
 // ---------------------------------------------------------------- planning
 struct Plan {
     int cfg;        // 0: 32x128 (M <= 32), 1: 64x128, 2: 128x128,
-                    // 4: streaming with in-workgroup K split (M <= 64)
+                    // 4: streaming with in-workgroup K split (M <= 64),
+                    // 5: 256x256 fp16-MFMA tiles (gemm_h16.hip)
     int mr;         // fold rows per 32-row block (cfg 0, 4)
     int splits;
     int groups_per_split;
@@ -649,6 +651,12 @@ struct Plan {
                                  // 101.5 -> 96.0 us; L70 M=128 (448 tiles) 216 us with 128x128, 230 without
 #ifndef WUSH_PF_BN
 #define WUSH_PF_BN 2             // and along N (2 x 2 wavefronts per workgroup)
+#endif
+#ifndef WUSH_H16_MIN_M
+#define WUSH_H16_MIN_M 512       // fp16-MFMA tiles from this M ...
+#endif
+#ifndef WUSH_H16_MIN_TILES
+#define WUSH_H16_MIN_TILES 256   // ... when they make at least this many 256x256 tiles (K % 256 == 0)
 #endif
 // 8 < M <= 32 streaming kernel (gemm_s4_stream32_kernel).  Measured on
 // MI355X against one wavefront per 32-row block: L70 (K=8192, N=57344)
@@ -734,6 +742,13 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         p.groups_per_split = (int)gps;
         return p;
     }
+    if (allow_split && K % 256 == 0 && M >= WUSH_H16_MIN_M &&
+        ((M + 255) / 256) * ((N + 255) / 256) >= WUSH_H16_MIN_TILES) {
+        p.cfg = 5; p.tm = 256; p.tn = 256; p.sg = 1;
+        p.splits = 1;
+        p.groups_per_split = (int)G0;
+        return p;
+    }
     const int64_t big_tiles = ((M + 32 * WUSH_PF_BM * 2 - 1) / (32 * WUSH_PF_BM * 2)) *
                               ((N + 32 * WUSH_PF_BN * 2 - 1) / (32 * WUSH_PF_BN * 2));
     if (M <= 32) {
@@ -785,6 +800,9 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     WUSH_REQUIRE((N + p.tn - 1) / p.tn <= 0x7fffffffLL && (M + p.tm - 1) / p.tm <= 65535);
     float* partial = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int m = (int)M, n = (int)N, k = (int)K;
+    if (p.cfg == 5) {
+        if constexpr (!PT) return launch_gemm_h16(xq, xs, wq, ws, y, m, n, k, stream);
+    }
     if (p.cfg == 4) {
         if constexpr (!PT) {
             dim3 grid((unsigned)((N + 31) / 32), (unsigned)p.splits);
