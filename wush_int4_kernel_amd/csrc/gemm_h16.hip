@@ -385,9 +385,177 @@ void gemm_h16_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restrict_
     }
 }
 
+
+// The same product with 8 wavefronts per workgroup (2 per SIMD): the MFMA
+// tiles are 128 x 64 per wavefront (2 x 4 wavefronts, 128 AGPR accumulators),
+// and wavefronts 0-3 convert the activation rows, 4-7 the weight columns.  A
+// second wavefront per SIMD lets the conversion VALU of one run beside the
+// MFMAs of the other, where a single wavefront issues them one after another.
+template <bool VEC>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restrict__ xs,
+                       const uint8_t* __restrict__ wq, const uint16_t* __restrict__ ws,
+                       uint16_t* __restrict__ y, int M, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    int* sh_e = reinterpret_cast<int*>(smem + 2 * kH16Buf);   // [0, 256) rows, [256, 512) columns
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int m0 = blockIdx.y * kH16Tile;
+    const int n0 = blockIdx.x * kH16Tile;
+    const int G = K >> 5;
+    const int K2 = K >> 1;
+
+    // conversion role (wavefront-uniform): operand, its row r in the tile
+    const bool wside = wave >= 4;
+    const int r = tid & 255;
+    const uint8_t* codes = wside ? wq : xq;
+    const int lim = (wside ? N : M) - 1;
+    const int base = wside ? n0 : m0;
+    const uint16_t* ps = (wside ? ws : xs) + (size_t)min(base + r, lim) * G;
+
+    uint32_t mx, mx2;
+    h16_row_max<VEC>(ps, ps, G, mx, mx2);
+    const int e = h16_shift(mx);
+    sh_e[tid] = e;
+
+    const int p4 = lane & 3;
+    const int wrow = base + (wave & 3) * 64 + (lane & ~3);
+    const uint8_t* qc[kH16Batch];
+#pragma unroll
+    for (int i = 0; i < kH16Batch; ++i) qc[i] = codes + (size_t)min(wrow + i, lim) * K2 + p4 * 16;
+
+    struct Batch {
+        uint4 c[kH16Batch];
+        uint32_t s[kH16Batch];
+    };
+    auto load_batch = [&](int b, Batch& rr) {
+        const int g0 = min(b * kH16Batch, G - kH16Batch) * 16;
+#pragma unroll
+        for (int i = 0; i < kH16Batch; ++i) rr.c[i] = *reinterpret_cast<const uint4*>(qc[i] + g0);
+        if constexpr (VEC) {
+            const uint2 v = *reinterpret_cast<const uint2*>(ps + min(b * kH16Batch, G - kH16Batch));
+            rr.s[0] = v.x; rr.s[1] = v.y;
+        } else {
+#pragma unroll
+            for (int i = 0; i < kH16Batch; ++i) rr.s[i] = ps[min(b * kH16Batch + i, G - 1)];
+        }
+    };
+    const bool odd1 = (lane & 1) != 0;
+    const bool odd2 = (lane & 2) != 0;
+    auto transpose = [&](uint4 (&x)[kH16Batch]) {
+        uint4 z[kH16Batch];
+#pragma unroll
+        for (int i = 0; i < kH16Batch; ++i) {
+            const bool own = ((i & 1) != 0) == odd1;
+            const uint4 o = x[i ^ 1];
+            z[i].x = h16_xchg<0xB1>(x[i].x, o.x, !own);
+            z[i].y = h16_xchg<0xB1>(x[i].y, o.y, !own);
+            z[i].z = h16_xchg<0xB1>(x[i].z, o.z, !own);
+            z[i].w = h16_xchg<0xB1>(x[i].w, o.w, !own);
+        }
+#pragma unroll
+        for (int i = 0; i < kH16Batch; ++i) {
+            const bool own = ((i & 2) != 0) == odd2;
+            const uint4 o = z[i ^ 2];
+            x[i].x = h16_xchg<0x4E>(z[i].x, o.x, !own);
+            x[i].y = h16_xchg<0x4E>(z[i].y, o.y, !own);
+            x[i].z = h16_xchg<0x4E>(z[i].z, o.z, !own);
+            x[i].w = h16_xchg<0x4E>(z[i].w, o.w, !own);
+        }
+    };
+
+    Batch R0, R1;
+    load_batch(0, R0);
+    load_batch(1, R1);
+
+    const int wofs = (wside ? kH16Op : 0) + (r >> 5) * 1024 + (r & 31) * 16;
+    auto convert = [&](int buf, Batch& rr, int i) {
+        if (i == 0) transpose(rr.c);
+        uint8_t* dst = smem + buf * kH16Buf + wofs;
+        h2 sc, sc16;
+        h16_scale(h16_batch_scale<VEC>(rr.s, i), e, sc, sc16);
+        const uint32_t w4[4] = {rr.c[i].x, rr.c[i].y, rr.c[i].z, rr.c[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<uint4*>(dst + (j >> 1) * kH16Slice + (j & 1) * 512) = h16_codes(w4[j], sc, sc16);
+    };
+
+    v16f acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16f){0.0f};
+
+    const int rba = (wave >> 2) * 4;             // this wavefront's first 32-row block
+    const int rbb = (wave & 3) * 2;              // ... and first 32-column block
+    auto compute = [&](int buf) {
+        const uint8_t* b0 = smem + buf * kH16Buf;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            h8 af[4], bf[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                af[i] = *reinterpret_cast<const h8*>(b0 + kk * kH16Slice + (rba + i) * 1024 + lane * 16);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                bf[j] = *reinterpret_cast<const h8*>(b0 + kH16Op + kk * kH16Slice + (rbb + j) * 1024 + lane * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    convert(0, R0, 0);
+    __syncthreads();
+
+    for (int s0 = 0; s0 < G; s0 += 2 * kH16Batch) {
+#pragma unroll
+        for (int j = 0; j < 2 * kH16Batch; ++j) {
+            compute(j & 1);
+            if (j < kH16Batch - 1) convert((j + 1) & 1, R0, j + 1);
+            else if (j == kH16Batch - 1) convert(0, R1, 0);
+            else if (j < 2 * kH16Batch - 1) convert((j + 1) & 1, R1, j + 1 - kH16Batch);
+            else convert(0, R0, 0);
+            if (j == kH16Batch - 1) load_batch(s0 / kH16Batch + 2, R0);
+            if (j == 2 * kH16Batch - 1) load_batch(s0 / kH16Batch + 3, R1);
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    const int half = lane >> 5;
+    const int l32 = lane & 31;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int cl = (rbb + j) * 32 + l32;
+        const int col = n0 + cl;
+        const int e_col = sh_e[256 + cl];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int rl = (rba + i) * 32 + 8 * (q >> 2) + 4 * half + (q & 3);
+                const int row = m0 + rl;
+                const int e_row = sh_e[rl];
+                float v = __builtin_ldexpf(acc[i][j][q], -(e_row + e_col));
+                if (e_row == kH16NonFinite || e_col == kH16NonFinite) v = __builtin_nanf("");
+                if (row < M && col < N) y[(size_t)row * N + col] = f32_to_f16_bits(v);
+            }
+        }
+    }
+}
+
 }  // namespace
 
 size_t gemm_h16_smem_bytes() { return 2 * kH16Buf + 2 * kH16Tile * sizeof(int); }
+
+#ifndef WUSH_H16_WAVES
+#define WUSH_H16_WAVES 8
+#endif
 
 int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                     uint16_t* y, int M, int N, int K, hipStream_t stream) {
@@ -396,20 +564,20 @@ int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     const bool vec = G % 8 == 0 && ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws)) & 15u) == 0;
     dim3 grid((unsigned)((N + kH16Tile - 1) / kH16Tile), (unsigned)((M + kH16Tile - 1) / kH16Tile));
     const size_t smem = gemm_h16_smem_bytes();
+    constexpr bool w8 = WUSH_H16_WAVES == 8;
+    auto kt = w8 ? &gemm_h16w8_kernel<true> : &gemm_h16_kernel<true>;
+    auto kf = w8 ? &gemm_h16w8_kernel<false> : &gemm_h16_kernel<false>;
     static bool attr_set = false;                // above the default 64 KiB of dynamic LDS
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_h16_kernel<true>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kt),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (e == hipSuccess)
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_h16_kernel<false>),
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(kf),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (e != hipSuccess) return (int)e;
         attr_set = true;
     }
-    if (vec)
-        gemm_h16_kernel<true><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, M, N, K);
-    else
-        gemm_h16_kernel<false><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, M, N, K);
+    (vec ? kt : kf)<<<grid, w8 ? 512 : 256, smem, stream>>>(xq, xs, wq, ws, y, M, N, K);
     return (int)hipGetLastError();
 }
 
