@@ -411,8 +411,8 @@ def test_gemm_random_shapes_all_paths(capi):
 
 
 # Shapes the planner sends to the 256x256 fp16-MFMA tiles (K % 256 == 0,
-# M >= 512, at least 256 tiles): ragged M and N, one and several load batches.
-H16_SHAPES = [(512, 32768, 256), (700, 30000, 512), (1030, 16400, 1024), (4096, 4096, 2048)]
+# M >= 256, at least 128 tiles): ragged M and N, one and several load batches.
+H16_SHAPES = [(512, 32768, 256), (700, 30000, 512), (1030, 16400, 1024), (4096, 4096, 2048), (300, 33000, 512)]
 
 
 def _sample(g, n, k):

@@ -652,11 +652,16 @@ struct Plan {
 #ifndef WUSH_PF_BN
 #define WUSH_PF_BN 2             // and along N (2 x 2 wavefronts per workgroup)
 #endif
+// fp16-MFMA 256x256 tiles (gemm_h16.hip) from this M when they make at least
+// this many tiles (K % 256 == 0).  Against the int8 tiles on MI355X: L70
+// M=256 (224 tiles) 249 vs 392 us, M=2048 K=N=4096 (128) 108 vs 128,
+// M=1024 K=N=8192 (128) 195 vs 217; below: L70 M=128 254 vs 238,
+// M=256 K=4096 N=24576 (96 tiles) 105 vs 100, M=512 K=N=8192 (64) 192 vs 138.
 #ifndef WUSH_H16_MIN_M
-#define WUSH_H16_MIN_M 512       // fp16-MFMA tiles from this M ...
+#define WUSH_H16_MIN_M 256
 #endif
 #ifndef WUSH_H16_MIN_TILES
-#define WUSH_H16_MIN_TILES 256   // ... when they make at least this many 256x256 tiles (K % 256 == 0)
+#define WUSH_H16_MIN_TILES 128
 #endif
 // 8 < M <= 32 streaming kernel (gemm_s4_stream32_kernel).  Measured on
 // MI355X against one wavefront per 32-row block: L70 (K=8192, N=57344)
