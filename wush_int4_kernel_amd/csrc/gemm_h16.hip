@@ -49,6 +49,9 @@ constexpr int kH16Op = 2 * kH16Slice;            // one group of one operand
 constexpr int kH16Buf = 2 * kH16Op;              // activations + weights of one group
 constexpr int kH16Batch = 4;                     // groups per global load batch
 constexpr int kH16NonFinite = 1 << 20;           // row/column shift marking a non-finite scale
+#ifndef WUSH_H16_XCD
+#define WUSH_H16_XCD 1                           // XCD-aware tile order in the 8-wavefront kernel
+#endif
 
 // Power of two that moves the largest |scale| of a row (bf16 bits mx, sign
 // cleared) into [2^12, 2^13): mx < 2^(e-126) for exponent field e.
@@ -137,15 +140,24 @@ __device__ __forceinline__ void h16_scale(float f, int shift, h2& s, h2& s16) {
 // (low nibble) or 1024 + 16 * (code + 8) (high nibble of a byte), both exact;
 // the subtraction leaves code or 16 * code exactly and the product with s or
 // s/16 is one exact fp16 rounding.
+// (a & b) | c in one v_bitop3_b32 (truth table 0xEA for src0 = a, src1 = b,
+// src2 = c); left to itself the compiler fuses the XOR below into the AND
+// instead and spends a v_or_b32 per pair.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t r;
+    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0xea" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 __device__ __forceinline__ uint4 h16_codes(uint32_t w, h2 s, h2 s16) {
     const uint32_t t = w ^ 0x88888888u;
     const uint32_t t8 = t >> 8;
     const h2 b0 = {(_Float16)1032.0f, (_Float16)1032.0f};
     const h2 b1 = {(_Float16)1152.0f, (_Float16)1152.0f};
-    const h2 p0 = __builtin_bit_cast(h2, (t & 0x000F000Fu) | 0x64006400u);
-    const h2 p1 = __builtin_bit_cast(h2, (t & 0x00F000F0u) | 0x64006400u);
-    const h2 p2 = __builtin_bit_cast(h2, (t8 & 0x000F000Fu) | 0x64006400u);
-    const h2 p3 = __builtin_bit_cast(h2, (t8 & 0x00F000F0u) | 0x64006400u);
+    const h2 p0 = __builtin_bit_cast(h2, and_or(t, 0x000F000Fu, 0x64006400u));
+    const h2 p1 = __builtin_bit_cast(h2, and_or(t, 0x00F000F0u, 0x64006400u));
+    const h2 p2 = __builtin_bit_cast(h2, and_or(t8, 0x000F000Fu, 0x64006400u));
+    const h2 p3 = __builtin_bit_cast(h2, and_or(t8, 0x00F000F0u, 0x64006400u));
     uint4 r;
     r.x = __builtin_bit_cast(uint32_t, (h2)((p0 - b0) * s));
     r.y = __builtin_bit_cast(uint32_t, (h2)((p1 - b1) * s16));
@@ -402,8 +414,24 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
+#if WUSH_H16_XCD
+    // Workgroup i runs on XCD i % 8.  When the column tiles split evenly
+    // over the 8 XCDs, XCD x takes column tiles x, x + 8, ... and walks all
+    // row tiles of one before the next, so the workgroups in flight on an XCD
+    // share a few weight tiles in its L2.
+    int tm = blockIdx.y, tn = blockIdx.x;
+    if ((gridDim.x & 7) == 0) {
+        const int id = blockIdx.y * gridDim.x + blockIdx.x;
+        const int slot = id >> 3;
+        tm = slot % gridDim.y;
+        tn = (slot / gridDim.y) * 8 + (id & 7);
+    }
+    const int m0 = tm * kH16Tile;
+    const int n0 = tn * kH16Tile;
+#else
     const int m0 = blockIdx.y * kH16Tile;
     const int n0 = blockIdx.x * kH16Tile;
+#endif
     const int G = K >> 5;
     const int K2 = K >> 1;
 
