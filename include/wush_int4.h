@@ -78,8 +78,13 @@ int wush_gemv_int4(const uint8_t *xq, const uint16_t *xs, const uint8_t *wq, con
  * plan that needs no more than it is given. */
 size_t wush_gemm_s4_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
-/* Group-scaled W4A4 GEMM on int8 MFMA, any M >= 1, K % 32 == 0:
- * same math as wush_gemv_int4, y (M, N) fp16.
+/* Group-scaled W4A4 GEMM, any M >= 1, K % 32 == 0: the product of
+ * wush_gemv_int4, y (M, N) fp16.  On int8 MFMA with exact int32 group dots,
+ * except for prefill shapes (K % 256 == 0, M >= 256, at least 128 tiles of
+ * 256x256), which run fp16 MFMA on code*scale operands (exact after a
+ * power-of-two shift per row and column) accumulated in fp32 over all of K.
+ * Both agree with the fp64 product to 2e-3 relative Frobenius (tested); a row
+ * or column with a non-finite scale gives NaN there.
  * Replaces w4a4_gemm_s4 (csrc/gemm_s4.cu:320-379) and the superseded
  * w4a4_gemm / _v1 / _v2 (csrc/gemm_int4.cu:89-130, csrc/gemm_wmma.cu:128-172,
  * csrc/gemm_wmma2.cu:141-181) that compute the same product. */

@@ -595,15 +595,17 @@ int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     constexpr bool w8 = WUSH_H16_WAVES == 8;
     auto kt = w8 ? &gemm_h16w8_kernel<true> : &gemm_h16_kernel<true>;
     auto kf = w8 ? &gemm_h16w8_kernel<false> : &gemm_h16_kernel<false>;
-    static bool attr_set = false;                // above the default 64 KiB of dynamic LDS
-    if (!attr_set) {
+    static bool attr_set[64] = {};               // per device: above the default 64 KiB of dynamic LDS
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (!attr_set[dev]) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kt),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (e == hipSuccess)
             e = hipFuncSetAttribute(reinterpret_cast<const void*>(kf),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (e != hipSuccess) return (int)e;
-        attr_set = true;
+        attr_set[dev] = true;
     }
     (vec ? kt : kf)<<<grid, w8 ? 512 : 256, smem, stream>>>(xq, xs, wq, ws, y, M, N, K);
     return (int)hipGetLastError();
