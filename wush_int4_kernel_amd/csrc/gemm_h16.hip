@@ -421,10 +421,10 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
     // share a few weight tiles in its L2.
     int tm = blockIdx.y, tn = blockIdx.x;
     if ((gridDim.x & 7) == 0) {
-        const int id = blockIdx.y * gridDim.x + blockIdx.x;
-        const int slot = id >> 3;
-        tm = slot % gridDim.y;
-        tn = (slot / gridDim.y) * 8 + (id & 7);
+        const uint64_t id = (uint64_t)blockIdx.y * gridDim.x + blockIdx.x;
+        const uint64_t slot = id >> 3;
+        tm = (int)(slot % gridDim.y);
+        tn = (int)((slot / gridDim.y) * 8 + (id & 7));
     }
     const int m0 = tm * kH16Tile;
     const int n0 = tn * kH16Tile;
