@@ -412,7 +412,9 @@ def test_gemm_random_shapes_all_paths(capi):
 
 # Shapes the planner sends to the 256x256 fp16-MFMA tiles (K % 256 == 0,
 # M >= 256, at least 128 tiles): ragged M and N, one and several load batches.
-H16_SHAPES = [(512, 32768, 256), (700, 30000, 512), (1030, 16400, 1024), (4096, 4096, 2048), (300, 33000, 512)]
+# The last two split K across workgroups (8 and 4 slices of 8 groups).
+H16_SHAPES = [(512, 32768, 256), (700, 30000, 512), (1030, 16400, 1024), (4096, 4096, 2048), (300, 33000, 512),
+              (600, 4096, 2048), (1030, 4096, 1024)]
 
 
 def _sample(g, n, k):
@@ -431,9 +433,10 @@ def _run_gemm_unaligned(capi, xq, xs, wq, ws):
     bx[1:1 + xs.size] = to_dev_bf16(xs).reshape(-1)
     bw[1:1 + ws.size] = to_dev_bf16(ws).reshape(-1)
     y = torch.empty(M, N, dtype=torch.float16, device="cuda")
-    assert capi.gemm_s4_workspace_bytes(M, N, K) == 0
+    wsb = capi.gemm_s4_workspace_bytes(M, N, K)
+    work = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
     capi.gemm_s4(dx.data_ptr(), bx.data_ptr() + 2, dw.data_ptr(), bw.data_ptr() + 2, y.data_ptr(),
-                 M, N, K, None, 0, _stream())
+                 M, N, K, work.data_ptr() if wsb else None, wsb, _stream())
     torch.cuda.synchronize()
     return f16_tensor_f64(y)
 

@@ -13,9 +13,12 @@ namespace wush {
 size_t gemm_h16_smem_bytes();
 
 // y = group-scaled product, M x N fp16, for M, N >= 1 and K % 256 == 0 (code
-// tensors 16-byte aligned, scales 2-byte aligned); hipErrorInvalidValue
-// otherwise.
+// tensors 16-byte aligned, scales 2-byte aligned).  splits > 1 splits K into
+// slices of groups_per_split groups (a multiple of 8) and writes fp32 partials
+// [split][M][N] to partial instead of y (the caller sums them).
+// hipErrorInvalidValue for arguments outside these limits.
 int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
-                    uint16_t* y, int M, int N, int K, hipStream_t stream);
+                    uint16_t* y, float* partial, int M, int N, int K, int splits, int groups_per_split,
+                    hipStream_t stream);
 
 }  // namespace wush

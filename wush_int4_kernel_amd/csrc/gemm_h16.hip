@@ -407,7 +407,8 @@ template <bool VEC>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restrict__ xs,
                        const uint8_t* __restrict__ wq, const uint16_t* __restrict__ ws,
-                       uint16_t* __restrict__ y, int M, int N, int K) {
+                       uint16_t* __restrict__ y, float* __restrict__ partial, int M, int N, int K,
+                       int groups_per_split) {
     extern __shared__ __align__(16) uint8_t smem[];
     int* sh_e = reinterpret_cast<int*>(smem + 2 * kH16Buf);   // [0, 256) rows, [256, 512) columns
 
@@ -432,8 +433,11 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
     const int m0 = blockIdx.y * kH16Tile;
     const int n0 = blockIdx.x * kH16Tile;
 #endif
-    const int G = K >> 5;
+    const int GR = K >> 5;                       // groups of a row
     const int K2 = K >> 1;
+    // K slice of this workgroup (blockIdx.z): groups [gb, gb + G), G % 8 == 0
+    const int gb = blockIdx.z * groups_per_split;
+    const int G = min(GR - gb, groups_per_split);
 
     // conversion role (wavefront-uniform): operand, its row r in the tile
     const bool wside = wave >= 4;
@@ -441,7 +445,7 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
     const uint8_t* codes = wside ? wq : xq;
     const int lim = (wside ? N : M) - 1;
     const int base = wside ? n0 : m0;
-    const uint16_t* ps = (wside ? ws : xs) + (size_t)min(base + r, lim) * G;
+    const uint16_t* ps = (wside ? ws : xs) + (size_t)min(base + r, lim) * GR + gb;
 
     uint32_t mx, mx2;
     h16_row_max<VEC>(ps, ps, G, mx, mx2);
@@ -452,7 +456,7 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
     const int wrow = base + (wave & 3) * 64 + (lane & ~3);
     const uint8_t* qc[kH16Batch];
 #pragma unroll
-    for (int i = 0; i < kH16Batch; ++i) qc[i] = codes + (size_t)min(wrow + i, lim) * K2 + p4 * 16;
+    for (int i = 0; i < kH16Batch; ++i) qc[i] = codes + (size_t)min(wrow + i, lim) * K2 + gb * 16 + p4 * 16;
 
     struct Batch {
         uint4 c[kH16Batch];
@@ -571,7 +575,12 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
                 const int e_row = sh_e[rl];
                 float v = __builtin_ldexpf(acc[i][j][q], -(e_row + e_col));
                 if (e_row == kH16NonFinite || e_col == kH16NonFinite) v = __builtin_nanf("");
-                if (row < M && col < N) y[(size_t)row * N + col] = f32_to_f16_bits(v);
+                if (row < M && col < N) {
+                    if (partial != nullptr)
+                        partial[((size_t)blockIdx.z * M + row) * N + col] = v;
+                    else
+                        y[(size_t)row * N + col] = f32_to_f16_bits(v);
+                }
             }
         }
     }
@@ -586,28 +595,41 @@ size_t gemm_h16_smem_bytes() { return 2 * kH16Buf + 2 * kH16Tile * sizeof(int); 
 #endif
 
 int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
-                    uint16_t* y, int M, int N, int K, hipStream_t stream) {
+                    uint16_t* y, float* partial, int M, int N, int K, int splits, int groups_per_split,
+                    hipStream_t stream) {
     const int G = K >> 5;
-    if (M <= 0 || N <= 0 || K <= 0 || K % 256 != 0) return (int)hipErrorInvalidValue;
+    if (M <= 0 || N <= 0 || K <= 0 || K % 256 != 0 || splits < 1 || groups_per_split % 8 != 0 ||
+        (long long)splits * groups_per_split < G || (splits > 1 && partial == nullptr))
+        return (int)hipErrorInvalidValue;
     const bool vec = G % 8 == 0 && ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws)) & 15u) == 0;
-    dim3 grid((unsigned)((N + kH16Tile - 1) / kH16Tile), (unsigned)((M + kH16Tile - 1) / kH16Tile));
+    dim3 grid((unsigned)((N + kH16Tile - 1) / kH16Tile), (unsigned)((M + kH16Tile - 1) / kH16Tile), (unsigned)splits);
     const size_t smem = gemm_h16_smem_bytes();
     constexpr bool w8 = WUSH_H16_WAVES == 8;
-    auto kt = w8 ? &gemm_h16w8_kernel<true> : &gemm_h16_kernel<true>;
-    auto kf = w8 ? &gemm_h16w8_kernel<false> : &gemm_h16_kernel<false>;
+    const void* kt = w8 ? reinterpret_cast<const void*>(&gemm_h16w8_kernel<true>)
+                        : reinterpret_cast<const void*>(&gemm_h16_kernel<true>);
+    const void* kf = w8 ? reinterpret_cast<const void*>(&gemm_h16w8_kernel<false>)
+                        : reinterpret_cast<const void*>(&gemm_h16_kernel<false>);
     static bool attr_set[64] = {};               // per device: above the default 64 KiB of dynamic LDS
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     if (!attr_set[dev]) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kt),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(kf),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        hipError_t e = hipFuncSetAttribute(kt, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e == hipSuccess) e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
         if (e != hipSuccess) return (int)e;
         attr_set[dev] = true;
     }
-    (vec ? kt : kf)<<<grid, w8 ? 512 : 256, smem, stream>>>(xq, xs, wq, ws, y, M, N, K);
+    if (w8) {
+        if (vec)
+            gemm_h16w8_kernel<true><<<grid, 512, smem, stream>>>(xq, xs, wq, ws, y, partial, M, N, K, groups_per_split);
+        else
+            gemm_h16w8_kernel<false><<<grid, 512, smem, stream>>>(xq, xs, wq, ws, y, partial, M, N, K, groups_per_split);
+    } else {
+        if (splits != 1) return (int)hipErrorInvalidValue;   // the 4-wavefront kernel has no K split
+        if (vec)
+            gemm_h16_kernel<true><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, M, N, K);
+        else
+            gemm_h16_kernel<false><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, M, N, K);
+    }
     return (int)hipGetLastError();
 }
 

@@ -661,7 +661,18 @@ struct Plan {
 #define WUSH_H16_MIN_M 256
 #endif
 #ifndef WUSH_H16_MIN_TILES
-#define WUSH_H16_MIN_TILES 128
+#define WUSH_H16_MIN_TILES 128       // workgroups, counting K slices
+#endif
+// K split of the fp16 tiles (fp32 partials in the workspace, summed by
+// splitk_reduce_kernel) from this M while fewer than 256 workgroups would run:
+// M=1024 K=N=4096 (64 tiles, 4 slices) 80 -> 67 us against the int8 tiles,
+// M=512 K=N=8192 135 -> 97, M=1024 K=N=8192 (128 tiles, 2 slices) 206 -> 163;
+// at M=256 it lost (K=4096 N=24576: 97 -> 112 us, 384 workgroups).
+#ifndef WUSH_H16_MAX_SPLITS
+#define WUSH_H16_MAX_SPLITS 8
+#endif
+#ifndef WUSH_H16_SPLIT_MIN_M
+#define WUSH_H16_SPLIT_MIN_M 512
 #endif
 // 8 < M <= 32 streaming kernel (gemm_s4_stream32_kernel).  Measured on
 // MI355X against one wavefront per 32-row block: L70 (K=8192, N=57344)
@@ -747,12 +758,20 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         p.groups_per_split = (int)gps;
         return p;
     }
-    if (allow_split && K % 256 == 0 && M >= WUSH_H16_MIN_M &&
-        ((M + 255) / 256) * ((N + 255) / 256) >= WUSH_H16_MIN_TILES) {
-        p.cfg = 5; p.tm = 256; p.tn = 256; p.sg = 1;
-        p.splits = 1;
-        p.groups_per_split = (int)G0;
-        return p;
+    if (allow_split && K % 256 == 0 && M >= WUSH_H16_MIN_M) {
+        // fp16-MFMA tiles, with K split across workgroups (slices of a
+        // multiple of 8 groups) while fewer than 256 workgroups would run
+        const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+        int s = 1;
+        while (M >= WUSH_H16_SPLIT_MIN_M && s < WUSH_H16_MAX_SPLITS && tiles * s < 256 && G0 % (16 * s) == 0 &&
+               (size_t)(2 * s) * (size_t)M * (size_t)N * sizeof(float) <= ws_bytes_available)
+            s *= 2;
+        if (tiles * s >= WUSH_H16_MIN_TILES) {
+            p.cfg = 5; p.tm = 256; p.tn = 256; p.sg = 1;
+            p.splits = s;
+            p.groups_per_split = (int)(G0 / s);
+            return p;
+        }
     }
     const int64_t big_tiles = ((M + 32 * WUSH_PF_BM * 2 - 1) / (32 * WUSH_PF_BM * 2)) *
                               ((N + 32 * WUSH_PF_BN * 2 - 1) / (32 * WUSH_PF_BN * 2));
@@ -806,7 +825,11 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     float* partial = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int m = (int)M, n = (int)N, k = (int)K;
     if (p.cfg == 5) {
-        if constexpr (!PT) return launch_gemm_h16(xq, xs, wq, ws, y, m, n, k, stream);
+        if constexpr (!PT) {
+            const int st = launch_gemm_h16(xq, xs, wq, ws, y, partial, m, n, k, p.splits, p.groups_per_split,
+                                           stream);
+            if (st != 0 || p.splits == 1) return st;
+        }
     }
     if (p.cfg == 4) {
         if constexpr (!PT) {
@@ -866,7 +889,7 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
             launch_gemm<1, 1, 1, 4, 8, 24, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
     } else if (p.cfg == 1) {
         launch_gemm<1, 2, 2, 2, 8, 32, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
-    } else {
+    } else if (p.cfg == 2) {
         launch_gemm<WUSH_PF_BM, WUSH_PF_BN, 2, 2, 4, 32, PT>(xq, xs, wq, ws, y, partial, m, n, k, p, alpha, alpha_dev, stream);
     }
     if (p.splits > 1) {
