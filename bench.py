@@ -1,33 +1,41 @@
 #!/usr/bin/env python3
 """Benchmark of the WUSH INT4 W4A4 layer on one MI355X.
 
-Metric: microseconds per layer, and speedup vs hipBLASLt
-bf16, for the Llama-70B FFN shape K=8192, N=57344 at M = 1 / 8 / 32 / 4096.
+Metric: microseconds per layer, and speedup vs hipBLASLt bf16,
+for the Llama-70B FFN shape K=8192, N=57344 at M = 1 / 8 / 32 / 4096.
 
 A "step" is one forward pass of the layer's hot path over one batch of
-synthetic activations, exactly as the reference's official bench chains it
+synthetic activations, chained as the reference's official bench does
 (reference bench/exp_p13_official.py:31-39; my_int4.chain.make_chain):
   M == 1 : fused_transform_quant_int4_smallm -> w4a4_gemv
   M <= 4 : fused_transform_quant_int4_smallm -> w4a4_gemv_multi
   M <= 32: fused_transform_quant_int4_smallm -> w4a4_gemm_s4
   else   : fused_transform_quant_int4_v3     -> w4a4_gemm_s4
 with the weights pre-quantized (W' = W T^-1, sigma-clip s4 + bf16 scales) and
-resident in HBM.  One HIP graph holds --graph-steps chains (12 by default), each on
-its own layer's weights and transform, cycling over --copies distinct weight copies
-(together they exceed the 256 MB MALL, so every step streams its weights from HBM),
-the way a model's decoder stack is captured in one graph; replays are timed and
-divided by the number of steps they hold, so the per-replay launch cost (about
-5 us on this part) is paid once per graph as in a model's decode step.  `value` is the M=1 layer time (the
-headline decode point); the other M are reported beside it, each with the
-hipBLASLt bf16 GEMM time at the same shape measured the same way.
+resident in HBM; every step works on its own layer's weights and transform,
+cycling over --copies distinct weight copies that together exceed the 256 MB
+MALL, so every step streams its weights from HBM.
+
+Timing of each M (the headline `value` is M = 1):
+  * `us`: exactly --steps layer steps in 5 groups (sizes differ by at most
+    one), each group one replay of a HIP graph that holds the group's steps,
+    timed with HIP events on the replay stream; the median per-step time over
+    the groups.  The device is synchronized before and after.
+  * `us_graph12`: a graph of 12 layer steps (a decoder stack's per-token
+    graph), median per step over 5 groups of replays.
+  * `us_1step`: the reference's method (exp_p13_official.py:15-29): a graph of
+    one step, median per step over 5 groups of replays, so every step also pays
+    the replay launch cost (about 5 us on this part).
+hipBLASLt bf16 at the same shape is timed the same three ways.
 
 Also reported: the roofline of the dominant kernel at M=1 (gemv_int4, HBM-
 bound; timed alone with HIP events on its launch stream), and the CPU
-baseline -- the reference's CPU path (rtn quant of x + dequantized fp32
-matmul) restated with the same torch ops in oracle/rtn_torch.py, timed on a
-16384-row weight sample on this host's cores and scaled to the full layer.
+baseline -- the reference's CPU path (rtn_int4 quant + dequantized fp32
+matmul) restated with the same torch ops in oracle/rtn_torch.py, on this
+host's cores: the L70 layer at M=1 on a bounded weight sample, and BASELINE
+config 1 (X fp16 16x4096, W fp16 4096x4096, seed 0) at full size.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep]
 """
 from __future__ import annotations
 
@@ -75,17 +83,115 @@ def parse():
     return ap.parse_args()
 
 
+FP16_PEAK_TFLOPS = 2500.0       # dense fp16 MFMA (the prefill kernel's instruction)
+
+
+def capture(fns):
+    """One HIP graph holding one call of each function, after two eager passes."""
+    import torch
+    for _ in range(2):
+        for fn in fns:
+            fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for fn in fns:
+            fn()
+    return g
+
+
+def group_sizes(steps: int, groups: int = 5):
+    """`steps` split into `groups` (at most `steps`) sizes that differ by at most one."""
+    n = max(1, min(groups, steps))
+    base, extra = divmod(steps, n)
+    return [base + (1 if i < extra else 0) for i in range(n)]
+
+
+def time_steps(make_graph, steps: int, warmup: int):
+    """Exactly `steps` layer steps in 5 groups, each group one replay of a graph
+    holding the group's steps (make_graph(n) -> graph of n steps), timed with
+    HIP events on the current stream, the device synchronized before and after.
+    Returns the median per-step seconds over the groups and the per-group values."""
+    import torch
+    sizes = group_sizes(steps)
+    graphs = {n: make_graph(n) for n in sorted(set(sizes))}
+    g0, done = graphs[sizes[0]], 0
+    while done < warmup:
+        g0.replay()
+        done += sizes[0]
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    marks = []
+    for n in sizes:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        graphs[n].replay()
+        e1.record(stream)
+        marks.append((e0, e1, n))
+    torch.cuda.synchronize()
+    per = [e0.elapsed_time(e1) * 1e-3 / n for e0, e1, n in marks]
+    del graphs
+    return statistics.median(per), per
+
+
+def time_med5(graph, steps_per_replay: int, reps: int):
+    """The reference's med5 (bench/exp_p13_official.py:15-23): 3 warm-up
+    replays, then 5 groups of `reps` replays, each group timed with HIP events;
+    median per-step seconds."""
+    import torch
+    for _ in range(3):
+        graph.replay()
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    marks = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+        marks.append((e0, e1))
+    torch.cuda.synchronize()
+    return statistics.median(e0.elapsed_time(e1) * 1e-3 / (reps * steps_per_replay) for e0, e1 in marks)
+
+
+def ref_reps(M: int) -> int:
+    """Replays per timing group of a one-step graph (bench/exp_p13_matrix.py:65)."""
+    return 100 if M <= 8 else (30 if M <= 64 else 8)
+
+
+def prefill_mfma(M: int, K: int) -> str:
+    """MFMA type of the w4a4_gemm_s4 kernel for M rows at the bench's shapes:
+    the fp16 tiles from M = 256 when K % 256 == 0 (every bench shape has at
+    least 16 column tiles of 256, which with M >= 256 meets the planner's
+    tile-count condition, except Qwen3-8B K=N=4096 below M = 2048), int8
+    otherwise."""
+    return "fp16" if M >= 256 and K % 256 == 0 else "int8"
+
+
 SWEEP_SHAPES = [("Qwen3-8B", 4096, 4096), ("Qwen3-8B", 4096, 24576), ("Qwen3-8B", 12288, 4096),
                 ("Llama-70B", 8192, 8192), ("Llama-70B", 8192, 57344)]
 SWEEP_MS = [1, 2, 4, 8, 16, 32, 64, 128, 256, 1024, 2048, 4096]
+# bench/exp_p13_matrix.py:32 (GEMM alone, K = 4096) and :53-54 (9 layer shapes, K = 4096)
+REF_GEMM_SHAPES = [(8, 4096), (64, 4096), (2048, 512), (4096, 4096)]
+REF_E2E_SHAPES = [(1, 4096), (2, 4096), (4, 4096), (8, 4096), (16, 4096), (32, 4096), (64, 4096),
+                  (2048, 512), (4096, 4096)]
 
 
 def sweep(args):
-    """The reference's performance matrix (bench/exp_p13_matrix.py:64-73): five
-    FFN shapes x M = 1..4096, the layer step of my_int4.chain (its dispatch by
-    M) against hipBLASLt fp16 (the reference's baseline) and bf16, all captured
-    --graph-steps steps per HIP graph over enough distinct weight copies to
-    exceed the 256 MB MALL (the reference replays one warm weight set)."""
+    """The reference's performance matrices:
+    * bench/exp_p13_official.py:42-44 -- five FFN shapes x M = 1..4096, the
+      layer step of my_int4.chain (its dispatch by M) against hipBLASLt fp16
+      (the reference's baseline) and bf16, --graph-steps steps per HIP graph
+      over enough distinct weight copies to exceed the 256 MB MALL (the
+      reference replays one warm weight set), median of 5 groups;
+    * bench/exp_p13_matrix.py:32-45 -- w4a4_gemm_s4 alone at (M, N) = (8,
+      4096), (64, 4096), (2048, 512), (4096, 4096), K = 4096, one step per
+      graph replay, median of 5 groups (the reference's method), against the
+      hipBLASLt GEMMs at the same shape;
+    * bench/exp_p13_matrix.py:53-73 -- the 9 layer shapes at K = 4096
+      (M = 1..64 at N = 4096, 2048 x 512, 4096 x 4096), one step per replay.
+    A table goes to stderr and one JSON line to stdout."""
     import torch
     from my_int4 import _C
     from my_int4.chain import make_chain
@@ -94,53 +200,35 @@ def sweep(args):
     dev = torch.device("cuda:0")
     torch.backends.cuda.preferred_blas_library("hipblaslt")
     gen = torch.Generator(device=dev).manual_seed(0)
-    rows = []
 
-    def capture(fns):
-        for _ in range(2):
-            for fn in fns:
-                fn()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for fn in fns:
-                fn()
-        return g
-
-    def timed(g, steps_per_replay, replays):
-        g.replay()
-        torch.cuda.synchronize()
-        t = time.perf_counter()
-        for _ in range(replays):
-            g.replay()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t) / (replays * steps_per_replay)
-
-    for model, K, N in SWEEP_SHAPES:
+    def weights(K, N, copies_bytes=300_000_000):
         W = (torch.randn(N, K, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
         Xc = torch.randn(256, K, generator=gen, device=dev)
         T64 = compute_wush_transform(Xc.double(), W.double())
         wq, ws = _C.quant_int4(transform_weights(W.double(), T64).to(torch.bfloat16).contiguous())
         T = T64.to(torch.bfloat16).contiguous()
-        ncopies = max(2, min(8, -(-300_000_000 // (N * K * 9 // 16))))
-        copies = [(wq, ws, T)] + [(wq.clone(), ws.clone(), T.clone()) for _ in range(ncopies - 1)]
-        nb = max(2, min(8, -(-300_000_000 // (N * K * 2))))
+        nc = max(2, min(8, -(-copies_bytes // (N * K * 9 // 16))))
+        copies = [(wq, ws, T)] + [(wq.clone(), ws.clone(), T.clone()) for _ in range(nc - 1)]
+        nb = max(2, min(8, -(-copies_bytes // (N * K * 2))))
         blas_w = [W] + [W.clone() for _ in range(nb - 1)]
-        half_w = [w.half() for w in blas_w]
+        return copies, blas_w, [w.half() for w in blas_w]
+
+    def graph_of(fns_for_step, n):
+        return capture([fns_for_step(i) for i in range(n)])
+
+    rows = []
+    for model, K, N in SWEEP_SHAPES:
+        copies, blas_w, half_w = weights(K, N)
+        nc, nb = len(copies), len(blas_w)
         for M in SWEEP_MS:
             X = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
-            gs = args.graph_steps
-            reps = max(1, int(2e-3 / max(1e-6, 2 * M * N * K / 1e15) / gs) + 1) if M > 64 else 20
-            g = capture([make_chain(X, c[2], c[0], c[1], M) for c in (copies[i % ncopies] for i in range(gs))])
-            t4 = timed(g, gs, reps)
-            del g
-            gb = capture([lambda Wc=blas_w[i % nb]: torch.matmul(X, Wc.t()) for i in range(gs)])
-            tb = timed(gb, gs, reps)
-            del gb
             X16 = X.half()
-            gh = capture([lambda Wc=half_w[i % nb]: torch.matmul(X16, Wc.t()) for i in range(gs)])
-            th = timed(gh, gs, reps)
-            del gh
+            gs = args.graph_steps
+            reps = max(1, -(-args.steps // gs)) if M <= 64 else 1
+            t4 = time_med5(graph_of(lambda i: make_chain(X, copies[i % nc][2], copies[i % nc][0],
+                                                         copies[i % nc][1], M), gs), gs, reps)
+            tb = time_med5(graph_of(lambda i: (lambda Wc=blas_w[i % nb]: torch.matmul(X, Wc.t())), gs), gs, reps)
+            th = time_med5(graph_of(lambda i: (lambda Wc=half_w[i % nb]: torch.matmul(X16, Wc.t())), gs), gs, reps)
             tf = 2 * M * N * K / 1e12
             rows.append({"model": model, "K": K, "N": N, "M": M, "int4_us": round(t4 * 1e6, 2),
                          "int4_tflops": round(tf / t4, 2), "hipblaslt_fp16_us": round(th * 1e6, 2),
@@ -148,9 +236,48 @@ def sweep(args):
                          "speedup_vs_bf16": round(tb / t4, 3)})
             log(f"{model:9s} K={K:5d} N={N:5d} M={M:5d} | int4 {t4 * 1e6:9.2f} us {tf / t4:7.1f} TF/s | "
                 f"fp16 {th * 1e6:9.2f} us | bf16 {tb * 1e6:9.2f} us | {th / t4:5.2f}x {tb / t4:5.2f}x")
-        del copies, blas_w, half_w, W, wq, ws
+        del copies, blas_w, half_w
         torch.cuda.empty_cache()
-    print(json.dumps({"sweep": "reference shape x M matrix (bench/exp_p13_matrix.py)", "rows": rows}))
+
+    # the reference's GEMM-alone table and 9 layer shapes, K = 4096, one step per replay
+    K = 4096
+    gemm_rows, e2e_rows = [], []
+    for M, N in REF_GEMM_SHAPES:
+        copies, blas_w, half_w = weights(K, N)
+        wq, ws, T = copies[0]
+        X = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+        xq, xs = _C.fused_transform_quant_int4_v3(X, T)
+        reps = ref_reps(M)
+        t4 = time_med5(capture([lambda: _C.w4a4_gemm_s4(xq, xs, wq, ws)]), 1, reps)
+        tb = time_med5(capture([lambda: torch.matmul(X, blas_w[0].t())]), 1, reps)
+        X16 = X.half()
+        th = time_med5(capture([lambda: torch.matmul(X16, half_w[0].t())]), 1, reps)
+        gemm_rows.append({"M": M, "N": N, "K": K, "w4a4_gemm_s4_us": round(t4 * 1e6, 2),
+                          "tflops": round(2 * M * N * K / t4 / 1e12, 2), "hipblaslt_fp16_us": round(th * 1e6, 2),
+                          "hipblaslt_bf16_us": round(tb * 1e6, 2), "speedup_vs_fp16": round(th / t4, 3),
+                          "speedup_vs_bf16": round(tb / t4, 3)})
+        log(f"GEMM alone {M:5d}x{N:5d}x{K}: {t4 * 1e6:8.2f} us | fp16 {th * 1e6:8.2f} | bf16 {tb * 1e6:8.2f} | "
+            f"{th / t4:5.2f}x {tb / t4:5.2f}x")
+        del copies, blas_w, half_w
+        torch.cuda.empty_cache()
+    for M, N in REF_E2E_SHAPES:
+        copies, blas_w, half_w = weights(K, N)
+        wq, ws, T = copies[0]
+        X = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+        X16 = X.half()
+        reps = ref_reps(M)
+        t4 = time_med5(capture([make_chain(X, T, wq, ws, M)]), 1, reps)
+        tb = time_med5(capture([lambda: torch.matmul(X, blas_w[0].t())]), 1, reps)
+        th = time_med5(capture([lambda: torch.matmul(X16, half_w[0].t())]), 1, reps)
+        e2e_rows.append({"M": M, "N": N, "K": K, "layer_us": round(t4 * 1e6, 2),
+                         "hipblaslt_fp16_us": round(th * 1e6, 2), "hipblaslt_bf16_us": round(tb * 1e6, 2),
+                         "speedup_vs_fp16": round(th / t4, 3), "speedup_vs_bf16": round(tb / t4, 3)})
+        log(f"layer {M:5d}x{N:5d}x{K}: {t4 * 1e6:8.2f} us | fp16 {th * 1e6:8.2f} | bf16 {tb * 1e6:8.2f} | "
+            f"{th / t4:5.2f}x {tb / t4:5.2f}x")
+        del copies, blas_w, half_w
+        torch.cuda.empty_cache()
+    print(json.dumps({"sweep": "reference matrices (bench/exp_p13_official.py, bench/exp_p13_matrix.py)",
+                      "rows": rows, "gemm_alone_k4096": gemm_rows, "layers_k4096": e2e_rows}))
 
 
 def layer_bytes(M, N, K):
@@ -223,35 +350,6 @@ def main():
 
     stream = torch.cuda.current_stream()
 
-    def chain_fn(X, wq_, ws_, T_, M):
-        # the reference's dispatch by M (bench/exp_p13_official.py:31-39)
-        return make_chain(X, T_, wq_, ws_, M)
-
-    def capture(fns):
-        """One HIP graph holding one layer step per function, the way a
-        model's decoder stack is captured: the per-replay launch overhead is
-        paid once per len(fns) steps."""
-        for _ in range(2):
-            for fn in fns:
-                fn()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for fn in fns:
-                fn()
-        return g
-
-    def time_graph(g, steps_per_replay, steps, warmup):
-        replays = max(1, steps // steps_per_replay)
-        for _ in range(max(1, warmup // steps_per_replay)):
-            g.replay()
-        torch.cuda.synchronize()
-        t = time.perf_counter()
-        for _ in range(replays):
-            g.replay()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t) / (replays * steps_per_replay)
-
     # -------------------------------------------------------- kernel-only mode
     if args.kernel_only:
         M = 1
@@ -281,13 +379,15 @@ def main():
         def launch_product(kind, M_, N_, K_, wq_, ws_, reps=3):
             xq_, xs_ = _C.quant_int4(activations_k(M_, K_))
             y_ = torch.empty(M_, N_, dtype=torch.float16, device=dev)
+            wsb = capi.gemm_s4_workspace_bytes(M_, N_, K_)
+            work = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
             for _ in range(reps):
                 if kind == "gemv":
                     capi.gemv_int4(xq_.data_ptr(), xs_.data_ptr(), wq_.data_ptr(), ws_.data_ptr(), y_.data_ptr(),
                                    M_, N_, K_, stream.cuda_stream)
                 else:
                     capi.gemm_s4(xq_.data_ptr(), xs_.data_ptr(), wq_.data_ptr(), ws_.data_ptr(), y_.data_ptr(),
-                                 M_, N_, K_, None, 0, stream.cuda_stream)
+                                 M_, N_, K_, work.data_ptr() if wsb else None, wsb, stream.cuda_stream)
 
         def activations_k(M_, K_):
             return torch.randn(M_, K_, generator=gdev, device=dev).to(torch.bfloat16)
@@ -313,38 +413,55 @@ def main():
         return
 
     # ------------------------------------------------------------- layer sweep
+    torch.backends.cuda.preferred_blas_library("hipblaslt")
+    blas_w = None if args.no_blas else [Wt, Wt.clone()]
     layers = {}
-    blas_w = None
+    gs = args.graph_steps
     for M in Ms:
         X = activations(M, gdev).to(torch.bfloat16).contiguous()
-        gsteps = [copies[i % len(copies)] for i in range(args.graph_steps)]
-        graph = capture([chain_fn(X, cq, cs, Tc, M) for cq, cs, Tc in gsteps])
-        steps = args.steps if M <= 64 else max(10, args.steps // 10)
-        warm = args.warmup if M <= 64 else max(3, args.warmup // 4)
-        t_int4 = time_graph(graph, args.graph_steps, steps, warm)
-        del graph
+
+        def chain_graph(n):
+            return capture([make_chain(X, copies[i % len(copies)][2], copies[i % len(copies)][0],
+                                       copies[i % len(copies)][1], M) for i in range(n)])
+
+        t_int4, per_group = time_steps(chain_graph, args.steps, args.warmup)
+        reps12 = max(1, -(-args.steps // gs)) if M <= 64 else 1
+        t12 = time_med5(chain_graph(gs), gs, reps12)
+        t1 = time_med5(chain_graph(1), 1, ref_reps(M))
+        mfma = prefill_mfma(M, K)
+        peak = FP16_PEAK_TFLOPS if mfma == "fp16" else INT8_PEAK_TOPS
+        tflops = 2 * M * N * K / t_int4 / 1e12
         entry = {
             "us": round(t_int4 * 1e6, 2),
+            "us_groups": [round(t * 1e6, 2) for t in per_group],
+            "us_graph12": round(t12 * 1e6, 2),
+            "us_1step": round(t1 * 1e6, 2),
             "chain": " -> ".join(route(M)),
             "layer_bytes": layer_bytes(M, N, K),
             "hbm_gbs": round(layer_bytes(M, N, K) / t_int4 / 1e9, 1),
             "hbm_frac": round(layer_bytes(M, N, K) / t_int4 / 1e9 / HBM_PEAK_GBS, 4),
-            "int8_tops": round(2 * M * N * K / t_int4 / 1e12, 2),
-            "int8_mfma_frac": round(2 * M * N * K / t_int4 / 1e12 / INT8_PEAK_TOPS, 4),
+            "mfma": mfma,
+            "mfma_tops": round(tflops, 2),
+            "mfma_frac": round(tflops / peak, 4),
         }
-        if not args.no_blas:
-            torch.backends.cuda.preferred_blas_library("hipblaslt")
-            if blas_w is None:
-                blas_w = [Wt] + [Wt.clone() for _ in range(1)]
-            Xb = X
-            bgraph = capture([lambda Wc=blas_w[i % len(blas_w)]: torch.matmul(Xb, Wc.t())
-                              for i in range(args.graph_steps)])
-            t_blas = time_graph(bgraph, args.graph_steps, steps, warm)
-            del bgraph
-            entry["hipblaslt_bf16_us"] = round(t_blas * 1e6, 2)
-            entry["speedup_vs_hipblaslt"] = round(t_blas / t_int4, 3)
+        if blas_w is not None:
+            def blas_graph(n):
+                return capture([lambda Wc=blas_w[i % len(blas_w)]: torch.matmul(X, Wc.t()) for i in range(n)])
+
+            tb, _ = time_steps(blas_graph, args.steps, args.warmup)
+            tb12 = time_med5(blas_graph(gs), gs, reps12)
+            tb1 = time_med5(blas_graph(1), 1, ref_reps(M))
+            entry.update({
+                "hipblaslt_bf16_us": round(tb * 1e6, 2),
+                "hipblaslt_bf16_us_graph12": round(tb12 * 1e6, 2),
+                "hipblaslt_bf16_us_1step": round(tb1 * 1e6, 2),
+                "speedup_vs_hipblaslt": round(tb / t_int4, 3),
+                "speedup_vs_hipblaslt_graph12": round(tb12 / t12, 3),
+                "speedup_vs_hipblaslt_1step": round(tb1 / t1, 3),
+            })
         layers[f"M={M}"] = entry
         log(f"[bench] M={M}: {entry}")
+        torch.cuda.empty_cache()
 
     # ---------------------------------------- the path's other ops, timed alone
     ops = {}
@@ -362,10 +479,7 @@ def main():
     Xc2 = acts_c(Mc).to(torch.bfloat16)
     Wc2 = torch.randn(Kc, Kc, generator=gc, device=dev, dtype=torch.float32) * 0.02
     Tc2 = compute_wush_transform(acts_c(512).double(), Wc2.double()).to(torch.bfloat16).contiguous()
-    reps = 10
-    g2 = capture([lambda: _C.fused_transform_quant_int4(Xc2, Tc2)] * reps)
-    t = time_graph(g2, reps, args.steps, args.warmup)
-    del g2
+    t = time_med5(capture([lambda: _C.fused_transform_quant_int4(Xc2, Tc2)] * 10), 10, 4)
     tq_bytes = 2 * Mc * Kc + 64 * Kc + Mc * Kc // 2 + Mc * Kc // 16
     tq_lane_ops = 32 * Mc * Kc          # one exact-product fma per MAC, 32 MACs per element
     ops["fused_tq_cfg2"] = {
@@ -375,15 +489,15 @@ def main():
         "valu_lane_ops": tq_lane_ops, "valu_frac": round(tq_lane_ops / t / VALU_PEAK_LANE_OPS, 4),
     }
     # a2/a3: quant_int4 of one Llama-70B weight tensor (N x K bf16), HBM-bound
-    g3 = capture([lambda: _C.quant_int4(Wt)] * 2)
-    t = time_graph(g3, 2, max(4, args.steps // 20), 2)
-    del g3
+    t = time_med5(capture([lambda: _C.quant_int4(Wt)] * 2), 2, 2)
     q_bytes = N * K * 2 + N * K // 2 + N * K // 16
     ops["quant_int4_l70_weights"] = {
         "us": round(t * 1e6, 2), "shape": f"{N}x{K} bf16", "hbm_bytes": q_bytes,
         "hbm_gbs": round(q_bytes / t / 1e9, 1), "hbm_frac": round(q_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
     }
     log(f"[bench] ops: {ops}")
+    del blas_w
+    torch.cuda.empty_cache()
 
     # --------------------------------------------- roofline of the M=1 kernel
     M = 1
@@ -445,9 +559,10 @@ def main():
         "data": "synthetic: seeded N(0,1) activations with 1% outlier channels x50, N(0,0.02) weights "
                 "transformed by this build's WUSH T and sigma-clip quantized",
         "config": {
-            "workload": f"Llama-70B FFN layer K={K} N={N}, M=1: fused_transform_quant_int4_smallm + w4a4_gemv, "
-                        f"one HIP graph of {args.graph_steps} layer steps cycling over {args.copies} "
-                        f"distinct weight copies",
+            "workload": f"Llama-70B FFN layer K={K} N={N}, M=1: fused_transform_quant_int4_smallm + w4a4_gemv; "
+                        f"{args.steps} layer steps timed as 5 graph replays of {'/'.join(map(str, sorted(set(group_sizes(args.steps)))))} "
+                        f"steps each (median per step), each step on its own weights cycling over {args.copies} "
+                        f"distinct copies",
             "K": K, "N": N, "M": 1,
         },
         "layers": layers,
@@ -459,15 +574,52 @@ def main():
     print(json.dumps(out))
 
 
+def _median_time(fn, reps=5):
+    fn()
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return statistics.median(ts)
+
+
+def cpu_config1(threads: int):
+    """BASELINE config 1 at full size on the host: X fp16 16x4096 ~ N(0,1) with
+    1% of the K channels x50, W fp16 4096x4096 ~ N(0,0.02), seed 0; quant(X),
+    quant(W) and dequant + fp32 matmul (my_int4/rtn_int4.py:33-75, restated in
+    oracle/rtn_torch.py), each the median of 5 after a warm-up, on `threads`
+    torch threads.  Returns seconds."""
+    import torch
+
+    from oracle import rtn_torch
+
+    g = torch.Generator().manual_seed(0)
+    M1, K1, N1 = 16, 4096, 4096
+    ch = torch.randperm(K1, generator=g)[:int(round(0.01 * K1))]
+    X = torch.randn(M1, K1, generator=g)
+    X[:, ch] *= 50.0
+    X = X.half()
+    W = (torch.randn(N1, K1, generator=g) * 0.02).half()
+    torch.set_num_threads(threads)
+    t_qx = _median_time(lambda: rtn_torch.quant(X))
+    t_qw = _median_time(lambda: rtn_torch.quant(W))
+    xq, xs = rtn_torch.quant(X)
+    wq, ws = rtn_torch.quant(W)
+    t_mm = _median_time(lambda: rtn_torch.w4a4_matmul(xq, xs, wq, ws))
+    return t_qx, t_qw, t_mm
+
+
 def cpu_baseline(wq, ws, X, N, K):
-    """The reference CPU path on this host for the L70 layer at M=1: rtn quant
-    of x, dequant of the weights and the fp32 matmul (my_int4/rtn_int4.py:33-75),
-    restated with the same eager torch CPU ops in oracle/rtn_torch.py (bit-
-    identical to the C oracle).  torch runs on the host's cores (at most 16, the
-    box's share per GPU).  Bounded sample: the first 16384 of the N weight rows,
-    median of 5 after a warm-up, scaled by N/16384 (dequant and matmul are
-    linear in N; the x quant is counted once).  A single-thread figure on a
-    2048-row sample is reported beside it."""
+    """The reference CPU path on this host (my_int4/rtn_int4.py:33-75, restated
+    with the same eager torch CPU ops in oracle/rtn_torch.py, bit-identical to
+    the C oracle), on the host's cores (at most 16, the box's share per GPU):
+    * the headline: the L70 layer at M=1 -- rtn quant of x, dequant of the
+      weights and the fp32 matmul -- on a bounded sample, the first 16384 of
+      the N weight rows, median of 5 after a warm-up, scaled by N/16384
+      (dequant and matmul are linear in N; the x quant is counted once); a
+      single-thread figure on a 2048-row sample beside it;
+    * BASELINE config 1 at full size (cpu_config1), on all threads and on one."""
     import torch
 
     from oracle import rtn_torch
@@ -478,32 +630,29 @@ def cpu_baseline(wq, ws, X, N, K):
     ws_c = ws[:S].cpu()
     x_c = X.cpu()
 
-    def med(fn, reps=5):
-        fn()
-        ts = []
-        for _ in range(reps):
-            t = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - t)
-        return statistics.median(ts)
-
     torch.set_num_threads(threads)
     xq, xs = rtn_torch.quant(x_c)
-    t_qx = med(lambda: rtn_torch.quant(x_c))
-    t_dw = med(lambda: rtn_torch.dequant(wq_c, ws_c))
+    t_qx = _median_time(lambda: rtn_torch.quant(x_c))
+    t_dw = _median_time(lambda: rtn_torch.dequant(wq_c, ws_c))
     wd = rtn_torch.dequant(wq_c, ws_c)
     xd = rtn_torch.dequant(xq, xs)
-    t_mm = med(lambda: xd @ wd.T)
+    t_mm = _median_time(lambda: xd @ wd.T)
     del wd
     per_layer = t_qx + (t_dw + t_mm) * (N / S)
     S1 = min(2048, N)
     torch.set_num_threads(1)
-    t1 = t_qx + med(lambda: rtn_torch.w4a4_matmul(xq, xs, wq_c[:S1], ws_c[:S1]), reps=3) * (N / S1)
+    t1 = t_qx + _median_time(lambda: rtn_torch.w4a4_matmul(xq, xs, wq_c[:S1], ws_c[:S1]), reps=3) * (N / S1)
+    c1_one = cpu_config1(1)
+    c1_all = cpu_config1(threads)
     torch.set_num_threads(threads)
     try:
         cpu_model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except Exception:
         cpu_model = platform.processor()
+
+    def ms(v):
+        return round(v * 1e3, 3)
+
     return {
         "value": round(per_layer * 1e6, 1),
         "unit": "us/layer",
@@ -513,6 +662,14 @@ def cpu_baseline(wq, ws, X, N, K):
                   f"fp32 matmul (oracle/rtn_torch.py, the reference's ops), {threads} threads, median of 5, "
                   f"scaled by N/{S}; per sample: quant {t_qx * 1e6:.0f} us, dequant {t_dw * 1e3:.1f} ms, "
                   f"matmul {t_mm * 1e3:.2f} ms; 1 thread: {t1 * 1e3:.0f} ms/layer ({S1}-row sample)",
+        "config1": {
+            "workload": "BASELINE config 1, full size: X fp16 16x4096 (1% channels x50), W fp16 4096x4096 "
+                        "N(0,0.02), seed 0; median of 5 after a warm-up each",
+            "threads": {str(threads): {"quant_x_ms": ms(c1_all[0]), "quant_w_ms": ms(c1_all[1]),
+                                       "dequant_matmul_ms": ms(c1_all[2])},
+                        "1": {"quant_x_ms": ms(c1_one[0]), "quant_w_ms": ms(c1_one[1]),
+                              "dequant_matmul_ms": ms(c1_one[2])}},
+        },
         "host": {"cpu_model": cpu_model, "os_cpu_count": os.cpu_count(), "torch_threads": threads},
     }
 

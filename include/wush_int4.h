@@ -42,6 +42,16 @@ enum wush_dtype {
 /* ABI version of the loaded library (WUSH_INT4_ABI_VERSION). */
 int wush_abi_version(void);
 
+/* One-time set-up of every visible device: the prefill kernel's dynamic LDS
+ * limit (a function attribute) and the decode GEMV's occupancy table.  Call
+ * it once before capturing any entry point in a HIP graph (the torch module
+ * calls it at import).  An entry point called on a device that was not set up
+ * runs the set-up there first, which sets a function attribute and so must not
+ * happen during a capture.  Thread-safe; returns the first error, or
+ * hipSuccess.  Replaces the reference's lazy static-flag attribute set-up
+ * (csrc/gemm_cutlass_int4.cu:62-67, :111-119). */
+int wush_init(void);
+
 /* Text for a status returned by any entry point. */
 const char *wush_error_string(int status);
 
@@ -105,8 +115,14 @@ int wush_mfma_selftest(const int8_t *a, const int8_t *b, int32_t *c, hipStream_t
 int wush_quant_int4_tensor_scale(const uint16_t *x, uint8_t *q, int64_t n, float inv_scale,
                                  const float *inv_scale_dev, hipStream_t stream);
 
+/* Largest K of wush_gemm_s4_tensor_scale: the int8 MFMA multiplies 16*code
+ * operands, so the int32 accumulator holds 256 * sum(qx*qw), up to
+ * 256 * 64 * K with codes of -8; 256 * 64 * 131040 < 2^31. */
+#define WUSH_TENSOR_SCALE_MAX_K 131040
+
 /* Per-tensor W4A4 GEMM: y = alpha * (xq @ wq^T) with an exact int32 dot over
- * all of K, y (M, N) fp16, K % 32 == 0.  alpha_dev, when not NULL, is a
+ * all of K, y (M, N) fp16, K % 32 == 0, K <= WUSH_TENSOR_SCALE_MAX_K (larger K
+ * is rejected with hipErrorInvalidValue).  alpha_dev, when not NULL, is a
  * device pointer to the fp32 alpha and overrides alpha.
  * Replaces w4a4_gemm_cutlass / _dev (csrc/gemm_cutlass_int4.cu:132-188). */
 int wush_gemm_s4_tensor_scale(const uint8_t *xq, const uint8_t *wq, uint16_t *y,

@@ -1,7 +1,8 @@
 """Exact-rational emulation of IEEE binary32 round-to-nearest-even.
 
 Used to pin the oracle independently of numpy and of the C compiler: every
-operation of the reference quantizer (my_int4/rtn_int4.py:22-55) is evaluated
+operation of the reference quantizer (my_int4/rtn_int4.py:22-55) and of the
+fused transform's sequential matvec (tests/test_sw2.py:12-24) is evaluated
 exactly with Fractions and then rounded by ``rn`` -- a separate implementation
 of the same specification, not a retyped formula.
 """
@@ -82,3 +83,22 @@ def quant_group(values) -> tuple[int, list[int]]:
     codes = [max(-7, min(7, rhe(rn(v / sb)))) for v in x]
     bits = struct.unpack("<I", struct.pack("<f", float(sb)))[0] >> 16
     return bits, codes
+
+
+def transform_block(x, T, order=None, fused=False) -> list[Fraction]:
+    """x'_j = sum_i x_i * T[j][i] for one 32-wide block of binary32 values x and
+    a 32 x 32 matrix T, with the reference's rounding (tests/test_sw2.py:18-22):
+    the accumulator starts at +0 and for i ascending takes RN(acc + RN(x_i *
+    T[j][i])).  `order` permutes the i sequence and `fused` rounds x_i*T+acc
+    once (an fma) -- both only to show that a check built on this function
+    notices a different order or contraction."""
+    xs = [Fraction(float(v)) for v in x]
+    idx = list(range(32)) if order is None else list(order)
+    out = []
+    for j in range(32):
+        acc = Fraction(0)
+        for i in idx:
+            prod = xs[i] * Fraction(float(T[j][i]))
+            acc = rn(acc + prod) if fused else rn(acc + rn(prod))
+        out.append(acc)
+    return out

@@ -482,6 +482,77 @@ def test_gemm_h16_int_exact_and_group_dots(capi):
         assert np.array_equal(y[np.ix_(rows, cols)], D[:, :, gg]), gg
 
 
+def _coarse_bf16(g, shape, emin, emax):
+    """bf16 bits of (1 + f/4) * 2^E, f in 0..3, E in [emin, emax]: two fraction
+    bits, so products of two scales and a group dot stay exact in fp32."""
+    f = g.integers(0, 4, shape)
+    E = g.integers(emin, emax + 1, shape)
+    return ((E + 127) << 7 | f << 5).astype(np.uint16)
+
+
+def test_gemm_h16_group_dots_nonunit_scales(capi):
+    # one group with non-unit scales, all others 0: y = fp16(sx * sw * D[:, :, g])
+    # exactly (the row's only nonzero scale is its largest, so every operand
+    # converts exactly and the fp32 sum of the 32 terms is exact)
+    g = rng(4515)
+    M, N, K = 512, 32768, 256
+    xq, _, wq, _ = _rand_operands(g, M, N, K)
+    rows, cols = _sample(g, M, 64), _sample(g, N, 2048)
+    D = oracle.group_dots(xq[rows], wq[cols]).astype(np.float64)
+    for gg in range(K // 32):
+        xs = np.zeros((M, K // 32), np.uint16)
+        ws = np.zeros((N, K // 32), np.uint16)
+        xs[:, gg] = _coarse_bf16(g, M, -8, 0)
+        ws[:, gg] = _coarse_bf16(g, N, -8, 0)
+        y = run_gemm(capi, xq, xs, wq, ws)[np.ix_(rows, cols)]
+        sx = bf16_bits_to_f32(xs[rows, gg]).astype(np.float64)
+        sw = bf16_bits_to_f32(ws[cols, gg]).astype(np.float64)
+        exact = (sx[:, None] * sw[None, :] * D[:, :, gg]).astype(np.float16).astype(np.float64)
+        assert np.array_equal(y, exact), gg
+
+
+def test_gemm_h16_group_scale_boundary(capi):
+    # One activation group at 2^-k of its row's largest scale (full 8-bit
+    # significands; the largest sits in group 0, whose codes are 0), one weight
+    # group nonzero.  The shifted largest scale lies in [2^12, 2^13), so the
+    # fp16 operand s/16 of the tested group keeps all 8 bits down to k = 25:
+    # y = fp16(sx * sw * D) exactly.  Below, s/16 rounds to fp16's subnormal
+    # spacing: each product term is off by at most 2^-27 * sx_max * sw_max,
+    # on top of the fp32 sum of 32 terms and the fp16 rounding of y.
+    g = rng(4516)
+    M, N, K = 512, 32768, 256
+    G = K // 32
+    xq, _, wq, _ = _rand_operands(g, M, N, K)
+    codes = unpack_codes(xq)
+    codes[:, :32] = 0
+    xq = pack_codes(codes)
+    rows, cols = _sample(g, M, 64), _sample(g, N, 2048)
+    D = oracle.group_dots(xq[rows], wq[cols]).astype(np.float64)
+    A = oracle.group_dots(pack_codes(np.abs(unpack_codes(xq[rows]))),
+                          pack_codes(np.abs(unpack_codes(wq[cols])))).astype(np.float64)
+    top = (((127 + g.integers(-2, 1, M)) << 7) | g.integers(0, 128, M)).astype(np.uint16)   # [0.25, 2)
+    for k in (22, 25, 26, 28, 33):
+        gg = 1 + k % (G - 1)
+        xs = np.zeros((M, G), np.uint16)
+        ws = np.zeros((N, G), np.uint16)
+        xs[:, 0] = top
+        xs[:, gg] = _bf16_times_pow2(top, -k)
+        ws[:, gg] = _coarse_bf16(g, N, -4, 0)
+        y = run_gemm(capi, xq, xs, wq, ws)[np.ix_(rows, cols)]
+        sx = bf16_bits_to_f32(xs[rows, gg]).astype(np.float64)
+        sw = bf16_bits_to_f32(ws[cols, gg]).astype(np.float64)
+        exact = sx[:, None] * sw[None, :] * D[:, :, gg]
+        if k <= 25:
+            assert np.array_equal(y, exact.astype(np.float16).astype(np.float64)), k
+        else:
+            sx_max = bf16_bits_to_f32(top[rows]).astype(np.float64)
+            ulp = np.spacing(np.abs(exact).astype(np.float16)).astype(np.float64)
+            bound = (0.5 * ulp + 32 * 2.0 ** -24 * sx[:, None] * sw[None, :] * A[:, :, gg]
+                     + 32 * 2.0 ** -27 * sx_max[:, None] * sw[None, :])
+            assert (np.abs(y - exact) <= bound).all(), k
+            assert np.count_nonzero(y) > 0, k
+
+
 def _bf16_times_pow2(bits, e):
     """bf16 bits of positive normal values times 2^e (e broadcast), exactly."""
     b = bits.astype(np.int64) + (np.asarray(e, np.int64) << 7)
@@ -593,6 +664,37 @@ def test_per_tensor_quant_and_gemm(capi):
         ref = oracle.gemm_tensor_scale_f64(xq, wq, alpha)
         assert rel_fro(f16_tensor_f64(y), ref) < FRO_TOL
         assert np.array_equal(f16_tensor_f64(y), f16_tensor_f64(y2))
+
+
+def test_per_tensor_largest_k(capi):
+    """K = 131040, the largest K the per-tensor GEMM admits (256 * 64 * K < 2^31):
+    codes of -8 in both operands put every int32 accumulator at its extreme,
+    256 * 64 * K; the result must equal the exact product (no wrap-around).
+    Random codes in [-8, 7] are checked against the fp64 oracle."""
+    import torch
+    from wush_int4_kernel_amd import capi as c
+    K = 131040
+    assert 256 * 64 * K < 2 ** 31
+    M, N = 4, 64
+    alpha = 2.0 ** -14
+    xq = pack_codes(np.full((M, K), -8))
+    wq = pack_codes(np.full((N, K), -8))
+    dx, dw = to_dev_u8(xq), to_dev_u8(wq)
+    y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    c.gemm_s4_tensor_scale(dx.data_ptr(), dw.data_ptr(), y.data_ptr(), M, N, K, alpha, None, _stream())
+    torch.cuda.synchronize()
+    exact = np.float16(64.0 * K * alpha)
+    assert np.all(y.cpu().numpy() == exact), (y.cpu().numpy()[0, :4], exact)
+    g = rng(6100)
+    xq = pack_codes(g.integers(-8, 8, (M, K)))
+    wq = pack_codes(g.integers(-8, 8, (N, K)))
+    dx, dw = to_dev_u8(xq), to_dev_u8(wq)
+    c.gemm_s4_tensor_scale(dx.data_ptr(), dw.data_ptr(), y.data_ptr(), M, N, K, 1.0 / 1024, None, _stream())
+    torch.cuda.synchronize()
+    ref = oracle.gemm_tensor_scale_f64(xq, wq, 1.0 / 1024)
+    assert rel_fro(f16_tensor_f64(y), ref) < FRO_TOL
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        c.gemm_s4_tensor_scale(dx.data_ptr(), dw.data_ptr(), y.data_ptr(), M, N, K + 32, 1.0, None, _stream())
 
 
 def test_invalid_arguments_rejected(capi):

@@ -77,6 +77,10 @@ def test_argument_validation_without_device(capi):
     assert lib.wush_gemv_int4(P(16), P(16), P(16), P(16), P(16), 8, 4, 1 << 20, None) == INVALID  # LDS
     assert lib.wush_gemm_s4(P(16), P(16), P(16), P(16), P(16), 4, 4, 40, None, 0, None) == INVALID
     assert lib.wush_gemm_s4_tensor_scale(P(16), P(16), P(16), 4, 4, 1 << 21, 1.0, None, None) == INVALID
+    # int32 bound of the per-tensor GEMM: 256 * 64 * K < 2^31 for K <= 131040
+    assert 256 * 64 * 131040 < 2 ** 31 <= 256 * 64 * (131040 + 32)
+    assert lib.wush_gemm_s4_tensor_scale(P(16), P(16), P(16), 4, 4, 131040 + 32, 1.0, None, None) == INVALID
+    assert lib.wush_gemm_s4_tensor_scale(P(16), P(16), P(16), 0, 4, 131040, 1.0, None, None) == 0  # empty, valid
     assert lib.wush_quant_int4_tensor_scale(P(16), P(16), 40, 1.0, None, None) == INVALID
     assert lib.wush_mfma_selftest(None, None, None, None) == INVALID
     assert b"invalid argument" in lib.wush_error_string(INVALID)

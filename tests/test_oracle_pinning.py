@@ -256,6 +256,42 @@ def test_transform_c_vs_numpy_random_T():
     assert np.allclose(xp, ref, rtol=1e-5, atol=1e-4 * np.abs(ref).max())
 
 
+def test_transform_rounding_order_exact_emulation():
+    # x'_j = RN(...RN(RN(x_0*T_j0) + RN(x_1*T_j1))...), i ascending, every
+    # product and sum rounded (tests/test_sw2.py:12-24), evaluated exactly
+    # with Fractions, then the exact quantizer: the C oracle's transform and
+    # fused codes/scales must match bit for bit.  Random bf16 T; reversing the
+    # order changes x' on this data, so the check sees the order.  A product of
+    # two bf16 values is exact in fp32, so contracting to an fma leaves x'
+    # unchanged here -- the equivalence the GPU kernel's fma loop relies on.
+    from _fp32_exact import transform_block
+    g = rng(24)
+    rows, K = 3, 128
+    xb = outlier_activations(g, rows, K)
+    tb = f32_to_bf16_bits(g.standard_normal((K // 32, 32, 32)) * 0.3)
+    xv, tv = bf16_bits_to_f32(xb), bf16_bits_to_f32(tb)
+    xp = oracle.transform(xb, tb)
+    q, s = oracle.fused_tq(xb, tb)
+    exact = np.zeros((rows, K), np.float32)
+    rev_differs, fma_same = False, False
+    for r in range(rows):
+        codes = []
+        for c in range(K // 32):
+            blk = transform_block(xv[r, c * 32:(c + 1) * 32], tv[c])
+            exact[r, c * 32:(c + 1) * 32] = [float(v) for v in blk]
+            bits, cq = exact_quant_group(exact[r, c * 32:(c + 1) * 32])
+            assert s[r, c] == bits, (r, c)
+            codes.extend(cq)
+            if r == 0 and c == 0:
+                rev = transform_block(xv[r, :32], tv[0], order=range(31, -1, -1))
+                fma = transform_block(xv[r, :32], tv[0], fused=True)
+                rev_differs = rev != blk
+                fma_same = fma == blk
+        assert np.array_equal(q[r], pack_codes(np.array(codes))), r
+    assert np.array_equal(xp.view(np.uint32), exact.view(np.uint32))
+    assert rev_differs and fma_same
+
+
 # ---------------------------------------------------------------------- GEMM
 def test_group_dots_brute_force():
     g = rng(31)

@@ -25,7 +25,7 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libwush_int4.so")
 EXT = os.path.join(PKG, "_C" + sysconfig.get_config_var("EXT_SUFFIX"))
 
-HIP_SOURCES = ["quant.hip", "fused_tq.hip", "gemv.hip", "gemm_s4.hip", "gemm_h16.hip"]
+HIP_SOURCES = ["quant.hip", "fused_tq.hip", "gemv.hip", "gemm_s4.hip", "gemm_h16.hip", "setup.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -44,13 +44,11 @@ HIPCC_FLAGS = [
 
 # MFMA results in VGPRs: the int8 kernels' fold reads every accumulator
 # element, and an AGPR destination would add one v_accvgpr_read per element.
-# gemm_h16.hip keeps its 256 accumulators per wavefront in AGPRs instead.
 VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
-AGPR_SOURCES = {"gemm_h16.hip"}
 
 
 def source_flags(src: str) -> list:
-    return HIPCC_FLAGS + ([] if src in AGPR_SOURCES else VGPR_FORM)
+    return HIPCC_FLAGS + VGPR_FORM
 
 
 def _run(cmd, verbose):
@@ -78,7 +76,7 @@ def build_capi(verbose: bool = False) -> str:
         _run([cc, *source_flags(src), f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj], verbose)
         return obj
 
-    with cf.ThreadPoolExecutor(max_workers=min(5, len(HIP_SOURCES))) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(6, len(HIP_SOURCES))) as ex:
         objs = list(ex.map(compile_one, HIP_SOURCES))
     tmp = LIB + ".tmp"
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)

@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(_PKG, "libwush_int4.so")
 _P, _I64, _I, _F, _SZ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
 SIGNATURES = {
     "wush_abi_version": ([], _I),
+    "wush_init": ([], _I),
     "wush_error_string": ([_I], ctypes.c_char_p),
     "wush_quant_int4": ([_P, _I, _P, _P, _I64, _P], _I),
     "wush_fused_tq": ([_P, _P, _P, _P, _I64, _I64, _P], _I),
@@ -45,6 +46,11 @@ def load() -> ctypes.CDLL:
             fn.restype = res
         _lib = lib
     return _lib
+
+
+def init() -> None:
+    """Per-device one-time set-up (call before capturing entry points in a graph)."""
+    _check(load().wush_init(), "wush_init")
 
 
 def _check(status: int, op: str) -> None:

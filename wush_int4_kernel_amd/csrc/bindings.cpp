@@ -271,6 +271,8 @@ torch::Tensor gemm_tensor_scale_impl(torch::Tensor xq, torch::Tensor wq, double 
     const int64_t M = xq.numel() / K2;
     TORCH_CHECK(M * K2 == xq.numel(), "xq numel must equal M*K/2 (K from wq)");
     TORCH_CHECK((2 * K2) % 32 == 0, "K must be a multiple of 32");
+    TORCH_CHECK(2 * K2 <= WUSH_TENSOR_SCALE_MAX_K, "K must be <= ", WUSH_TENSOR_SCALE_MAX_K,
+                " (the per-tensor GEMM's int32 accumulator holds 256 * sum(qx * qw))");
     const int64_t N = wq.size(0);
     const at::hip::OptionalHIPGuardMasqueradingAsCUDA guard(xq.device());
     auto y = torch::empty({M, N}, torch::dtype(torch::kHalf).device(xq.device()));
@@ -296,6 +298,11 @@ torch::Tensor w4a4_gemm_cutlass_dev(torch::Tensor xq, torch::Tensor wq, torch::T
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.doc() = "my_int4._C on MI355X: HIP/gfx950 kernels behind the reference op signatures";
+    // One-time per-device set-up (launch attributes, occupancy tables) at
+    // import, so that no op run inside a HIP graph capture has to do it.
+    // Without a GPU this reports hipErrorNoDevice; the ops then report errors
+    // themselves when called.
+    m.attr("setup_status") = wush_init();
     m.def("quant_int4_tensor_scale", &quant_int4_tensor_scale, "Per-tensor INT4 quantize",
           py::arg("x"), py::arg("scale"));
     m.def("quant_int4_tensor_scale_dev", &quant_int4_tensor_scale_dev,

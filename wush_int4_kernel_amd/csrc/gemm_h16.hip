@@ -21,10 +21,10 @@
 // row's largest scale per term).  A row or column with a non-finite scale
 // gives NaN, as the reference's dequantized product does (code 0 * inf).
 //
-// Workgroup: 4 wavefronts in 2 x 2, a 256 x 256 output tile, each wavefront
-// 128 x 128 (16 accumulator blocks, 256 AGPRs), one workgroup per CU.  A stage
-// is one group (K = 32): thread t converts row t of the activation tile and
-// column t of the weight tile (16 code bytes each) to fp16 in a
+// Workgroup: 8 wavefronts in 2 x 4, a 256 x 256 output tile, each wavefront
+// 128 x 64 (8 accumulator blocks), one workgroup per CU.  A stage is one
+// group (K = 32): thread t converts row t of the activation tile (t < 256)
+// or column t - 256 of the weight tile (16 code bytes each) to fp16 in a
 // double-buffered LDS tile laid out fragment-major, [K16 slice][32-row block]
 // [k-half][row][8 halves], so that a wavefront's operand read of one 32-row
 // block is 1 KiB contiguous (lane l at 16*l) and the conversion writes of
@@ -35,6 +35,7 @@
 // has no conditional loads.
 #include "wush_device.h"
 #include "gemm_h16.h"
+#include "setup.h"
 
 namespace wush {
 namespace {
@@ -178,13 +179,6 @@ __device__ __forceinline__ uint32_t h16_xchg(uint32_t keep, uint32_t other, bool
     return take_other ? v : keep;
 }
 
-struct H16Batch {
-    uint4 a[kH16Batch];
-    uint4 b[kH16Batch];
-    uint32_t sa[kH16Batch];
-    uint32_t sb[kH16Batch];
-};
-
 // fp32 value of scale i of a batch (bits are only re-read here, at the
 // conversion, so the load's wait lands there too)
 template <bool VEC>
@@ -193,216 +187,11 @@ __device__ __forceinline__ float h16_batch_scale(const uint32_t (&v)[kH16Batch],
     return __uint_as_float(v[i] << 16);
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void gemm_h16_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restrict__ xs,
-                     const uint8_t* __restrict__ wq, const uint16_t* __restrict__ ws,
-                     uint16_t* __restrict__ y, int M, int N, int K) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    int* sh_ea = reinterpret_cast<int*>(smem + 2 * kH16Buf);
-    int* sh_eb = sh_ea + kH16Tile;
-
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lane = tid & 63;
-    const int m0 = blockIdx.y * kH16Tile;
-    const int n0 = blockIdx.x * kH16Tile;
-    const int G = K >> 5;
-    const int K2 = K >> 1;
-
-    // this thread's activation row and weight column for the scales (clamped:
-    // rows past the end load valid data and are never stored)
-    const int ra = min(m0 + tid, M - 1);
-    const int rb = min(n0 + tid, N - 1);
-    const uint16_t* psa = xs + (size_t)ra * G;
-    const uint16_t* psb = ws + (size_t)rb * G;
-
-    // Code loads, coalesced: lane (q, p) = (lane / 4, lane % 4) reads 16
-    // bytes of group 4b + p of the wavefront's rows 4q + i (i = 0..3), so one
-    // load instruction covers 16 rows x 64 contiguous bytes.  Lane (q, p)
-    // then holds X[i] = (row 4q+i, group p); h16_transpose turns that into
-    // (row 4q+p = its own row, group i) at the batch's first conversion.
-    const int p4 = lane & 3;
-    const int wrow = m0 + wave * 64 + (lane & ~3);   // row of X[0] in the activation tile
-    const int wcol = n0 + wave * 64 + (lane & ~3);
-    const uint8_t* qa[kH16Batch];
-    const uint8_t* qb[kH16Batch];
-#pragma unroll
-    for (int i = 0; i < kH16Batch; ++i) {
-        qa[i] = xq + (size_t)min(wrow + i, M - 1) * K2 + p4 * 16;
-        qb[i] = wq + (size_t)min(wcol + i, N - 1) * K2 + p4 * 16;
-    }
-    auto load_batch = [&](int b, H16Batch& r) {
-        // G % 8 == 0: a batch never straddles the end of a row; the clamp
-        // keeps the loads of batches past the end inside the last one
-        const int g0 = min(b * kH16Batch, G - kH16Batch) * 16;
-#pragma unroll
-        for (int i = 0; i < kH16Batch; ++i) {
-            r.a[i] = *reinterpret_cast<const uint4*>(qa[i] + g0);
-            r.b[i] = *reinterpret_cast<const uint4*>(qb[i] + g0);
-        }
-        if constexpr (VEC) {
-            const int g = min(b * kH16Batch, G - kH16Batch);
-            const uint2 va = *reinterpret_cast<const uint2*>(psa + g);
-            const uint2 vb = *reinterpret_cast<const uint2*>(psb + g);
-            r.sa[0] = va.x; r.sa[1] = va.y;
-            r.sb[0] = vb.x; r.sb[1] = vb.y;
-        } else {
-#pragma unroll
-            for (int i = 0; i < kH16Batch; ++i) {
-                const int g = min(b * kH16Batch + i, G - 1);
-                r.sa[i] = psa[g];
-                r.sb[i] = psb[g];
-            }
-        }
-    };
-
-    // 4 x 4 transpose of the batch's code chunks across the lanes of a quad
-    // (butterflies over lane bit 0, then bit 1): afterwards a[i] / b[i] hold
-    // group i of this lane's own row / column.
-    const bool odd1 = (lane & 1) != 0;
-    const bool odd2 = (lane & 2) != 0;
-    auto transpose = [&](uint4 (&x)[kH16Batch]) {
-        uint4 z[kH16Batch];
-#pragma unroll
-        for (int i = 0; i < kH16Batch; ++i) {
-            const bool own = ((i & 1) != 0) == odd1;
-            const uint4 o = x[i ^ 1];
-            z[i].x = h16_xchg<0xB1>(x[i].x, o.x, !own);
-            z[i].y = h16_xchg<0xB1>(x[i].y, o.y, !own);
-            z[i].z = h16_xchg<0xB1>(x[i].z, o.z, !own);
-            z[i].w = h16_xchg<0xB1>(x[i].w, o.w, !own);
-        }
-#pragma unroll
-        for (int i = 0; i < kH16Batch; ++i) {
-            const bool own = ((i & 2) != 0) == odd2;
-            const uint4 o = z[i ^ 2];
-            x[i].x = h16_xchg<0x4E>(z[i].x, o.x, !own);
-            x[i].y = h16_xchg<0x4E>(z[i].y, o.y, !own);
-            x[i].z = h16_xchg<0x4E>(z[i].z, o.z, !own);
-            x[i].w = h16_xchg<0x4E>(z[i].w, o.w, !own);
-        }
-    };
-
-    // row shifts first: their loads are waited for here, so the batch loads
-    // below start the main loop's load pattern with nothing else in flight
-    uint32_t mxa, mxb;
-    h16_row_max<VEC>(psa, psb, G, mxa, mxb);
-    const int ea = h16_shift(mxa);
-    const int eb = h16_shift(mxb);
-    sh_ea[tid] = ea;
-    sh_eb[tid] = eb;
-
-    H16Batch R0, R1;
-    load_batch(0, R0);
-    load_batch(1, R1);
-
-    // conversion writes: row tid of each operand, u32 j of the group's 16
-    // code bytes -> K16 slice j/2, k-half j%2
-    const int wofs = (tid >> 5) * 1024 + (tid & 31) * 16;
-    auto convert = [&](int buf, H16Batch& r, int i) {
-        if (i == 0) {
-            transpose(r.a);
-            transpose(r.b);
-        }
-        uint8_t* base = smem + buf * kH16Buf;
-        h2 s, s16;
-        h16_scale(h16_batch_scale<VEC>(r.sa, i), ea, s, s16);
-        const uint32_t wa[4] = {r.a[i].x, r.a[i].y, r.a[i].z, r.a[i].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<uint4*>(base + (j >> 1) * kH16Slice + (j & 1) * 512 + wofs) = h16_codes(wa[j], s, s16);
-        h16_scale(h16_batch_scale<VEC>(r.sb, i), eb, s, s16);
-        const uint32_t wb[4] = {r.b[i].x, r.b[i].y, r.b[i].z, r.b[i].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<uint4*>(base + kH16Op + (j >> 1) * kH16Slice + (j & 1) * 512 + wofs) =
-                h16_codes(wb[j], s, s16);
-    };
-
-    v16f acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = (v16f){0.0f};
-
-    const int rba = (wave >> 1) * 4;             // first 32-row block of this wavefront's activations
-    const int rbb = (wave & 1) * 4;              // ... and weight columns
-    auto compute = [&](int buf) {
-        const uint8_t* base = smem + buf * kH16Buf;
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            h8 af[4], bf[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                af[i] = *reinterpret_cast<const h8*>(base + kk * kH16Slice + (rba + i) * 1024 + lane * 16);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                bf[i] = *reinterpret_cast<const h8*>(base + kH16Op + kk * kH16Slice + (rbb + i) * 1024 + lane * 16);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-    };
-
-    convert(0, R0, 0);
-    __syncthreads();
-
-    // Stage s computes group s from buffer s&1 and converts group s+1 into
-    // the other buffer; batch b's registers are reloaded with batch b+2 right
-    // after their last group is converted.  G % 8 == 0, so the loop has one
-    // exit (exits from inside the unrolled body make the register allocator
-    // spill the batch registers); the last stage converts a clamped copy of
-    // group G-1 that is never computed.
-    for (int s0 = 0; s0 < G; s0 += 2 * kH16Batch) {
-#pragma unroll
-        for (int j = 0; j < 2 * kH16Batch; ++j) {
-            compute(j & 1);
-            if (j < kH16Batch - 1) convert((j + 1) & 1, R0, j + 1);
-            else if (j == kH16Batch - 1) convert(0, R1, 0);
-            else if (j < 2 * kH16Batch - 1) convert((j + 1) & 1, R1, j + 1 - kH16Batch);
-            else convert(0, R0, 0);
-            if (j == kH16Batch - 1) load_batch(s0 / kH16Batch + 2, R0);
-            if (j == 2 * kH16Batch - 1) load_batch(s0 / kH16Batch + 3, R1);
-            __syncthreads();
-            // keep each stage's work between its barriers: the scheduler
-            // would otherwise hoist the conversion of freshly loaded groups
-            // next to their loads and wait out the memory latency there
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-
-    // epilogue: y = acc * 2^-(ea + eb), NaN for a non-finite scale
-    const int half = lane >> 5;
-    const int l32 = lane & 31;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int cl = (rbb + j) * 32 + l32;
-        const int col = n0 + cl;
-        const int e_col = sh_eb[cl];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int rl = (rba + i) * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
-                const int row = m0 + rl;
-                const int e_row = sh_ea[rl];
-                float v = __builtin_ldexpf(acc[i][j][e], -(e_row + e_col));
-                if (e_row == kH16NonFinite || e_col == kH16NonFinite) v = __builtin_nanf("");
-                if (row < M && col < N) y[(size_t)row * N + col] = f32_to_f16_bits(v);
-            }
-        }
-    }
-}
-
-
-// The same product with 8 wavefronts per workgroup (2 per SIMD): the MFMA
-// tiles are 128 x 64 per wavefront (2 x 4 wavefronts, 128 AGPR accumulators),
-// and wavefronts 0-3 convert the activation rows, 4-7 the weight columns.  A
-// second wavefront per SIMD lets the conversion VALU of one run beside the
-// MFMAs of the other, where a single wavefront issues them one after another.
+// 8 wavefronts per workgroup (2 per SIMD): the MFMA tiles are 128 x 64 per
+// wavefront (2 x 4 wavefronts, 128 fp32 accumulators), and wavefronts 0-3
+// convert the activation rows, 4-7 the weight columns.  A second wavefront
+// per SIMD lets the conversion VALU of one run beside the MFMAs of the other
+// (with 4 wavefronts of 128 x 128, L70 M=4096 took 4.51 ms against 3.75).
 template <bool VEC>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restrict__ xs,
@@ -590,46 +379,36 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
 
 size_t gemm_h16_smem_bytes() { return 2 * kH16Buf + 2 * kH16Tile * sizeof(int); }
 
-#ifndef WUSH_H16_WAVES
-#define WUSH_H16_WAVES 8
-#endif
+int gemm_h16_init_device() {
+    // the workgroup's LDS is above the default 64 KiB limit of dynamic LDS
+    const int smem = (int)gemm_h16_smem_bytes();
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_h16w8_kernel<true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_h16w8_kernel<false>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+    return (int)e;
+}
 
 int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                     uint16_t* y, float* partial, int M, int N, int K, int splits, int groups_per_split,
                     hipStream_t stream) {
     const int G = K >> 5;
-    if (M <= 0 || N <= 0 || K <= 0 || K % 256 != 0 || splits < 1 || groups_per_split % 8 != 0 ||
-        (long long)splits * groups_per_split < G || (splits > 1 && partial == nullptr))
+    // every K slice holds a positive multiple of 8 groups
+    if (M <= 0 || N <= 0 || K <= 0 || K % 256 != 0 || splits < 1 || groups_per_split <= 0 ||
+        groups_per_split % 8 != 0 || (long long)splits * groups_per_split < G ||
+        (long long)(splits - 1) * groups_per_split >= G || (splits > 1 && partial == nullptr))
         return (int)hipErrorInvalidValue;
+    int dev = 0;
+    const int st = device_setup(&dev);
+    if (st != 0) return st;
     const bool vec = G % 8 == 0 && ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws)) & 15u) == 0;
     dim3 grid((unsigned)((N + kH16Tile - 1) / kH16Tile), (unsigned)((M + kH16Tile - 1) / kH16Tile), (unsigned)splits);
     const size_t smem = gemm_h16_smem_bytes();
-    constexpr bool w8 = WUSH_H16_WAVES == 8;
-    const void* kt = w8 ? reinterpret_cast<const void*>(&gemm_h16w8_kernel<true>)
-                        : reinterpret_cast<const void*>(&gemm_h16_kernel<true>);
-    const void* kf = w8 ? reinterpret_cast<const void*>(&gemm_h16w8_kernel<false>)
-                        : reinterpret_cast<const void*>(&gemm_h16_kernel<false>);
-    static bool attr_set[64] = {};               // per device: above the default 64 KiB of dynamic LDS
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    if (!attr_set[dev]) {
-        hipError_t e = hipFuncSetAttribute(kt, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-        if (e == hipSuccess) e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-        if (e != hipSuccess) return (int)e;
-        attr_set[dev] = true;
-    }
-    if (w8) {
-        if (vec)
-            gemm_h16w8_kernel<true><<<grid, 512, smem, stream>>>(xq, xs, wq, ws, y, partial, M, N, K, groups_per_split);
-        else
-            gemm_h16w8_kernel<false><<<grid, 512, smem, stream>>>(xq, xs, wq, ws, y, partial, M, N, K, groups_per_split);
-    } else {
-        if (splits != 1) return (int)hipErrorInvalidValue;   // the 4-wavefront kernel has no K split
-        if (vec)
-            gemm_h16_kernel<true><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, M, N, K);
-        else
-            gemm_h16_kernel<false><<<grid, 256, smem, stream>>>(xq, xs, wq, ws, y, M, N, K);
-    }
+    if (vec)
+        gemm_h16w8_kernel<true><<<grid, 512, smem, stream>>>(xq, xs, wq, ws, y, partial, M, N, K, groups_per_split);
+    else
+        gemm_h16w8_kernel<false><<<grid, 512, smem, stream>>>(xq, xs, wq, ws, y, partial, M, N, K, groups_per_split);
     return (int)hipGetLastError();
 }
 

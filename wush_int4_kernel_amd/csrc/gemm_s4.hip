@@ -927,7 +927,9 @@ int wush_gemm_s4(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const
 int wush_gemm_s4_tensor_scale(const uint8_t* xq, const uint8_t* wq, uint16_t* y, int64_t M, int64_t N,
                               int64_t K, float alpha, const float* alpha_dev, hipStream_t stream) {
     WUSH_REQUIRE(M >= 0 && N >= 0 && K > 0 && K % 32 == 0);
-    WUSH_REQUIRE(M <= 0x7fffffffLL && N <= 0x7fffffffLL && K <= (1LL << 20));
+    // the MFMA accumulates products of 16*code operands, 256 * 64 per k at
+    // most (codes -8 * -8): the int32 sum over K stays exact up to this K
+    WUSH_REQUIRE(M <= 0x7fffffffLL && N <= 0x7fffffffLL && K <= WUSH_TENSOR_SCALE_MAX_K);
     if (M == 0 || N == 0) return (int)hipSuccess;
     WUSH_REQUIRE(xq && wq && y);
     WUSH_REQUIRE(((uintptr_t)xq & 15u) == 0 && ((uintptr_t)wq & 15u) == 0 && ((uintptr_t)y & 1u) == 0);

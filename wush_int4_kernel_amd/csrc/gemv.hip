@@ -18,6 +18,7 @@
 // next chunk is requested before the current one is reduced, so each lane
 // keeps 2 x R x (K/2048) 16-byte loads outstanding.
 #include "wush_device.h"
+#include "setup.h"
 #include "../../include/wush_int4.h"
 
 namespace wush {
@@ -34,9 +35,6 @@ namespace wush {
 #endif
 template <int M>
 constexpr int gemv_waves() { return M == 1 ? WUSH_GEMV_WAVES : M >= 7 ? WUSH_GEMV_WAVES_M78 : WUSH_GEMV_WAVES_M; }
-#ifndef WUSH_GEMV_RS
-#define WUSH_GEMV_RS 1          // recursive-halving reduction of the R x M outputs
-#endif
 #ifndef WUSH_GEMV_TBAR
 #define WUSH_GEMV_TBAR 1        // scheduling barrier after each group (fewer live VGPRs)
 #endif
@@ -86,9 +84,9 @@ constexpr int pow2_ceil(int v) { return v <= 1 ? 1 : 2 * pow2_ceil((v + 1) / 2);
 template <int M, int R>
 __device__ __forceinline__ void store_outputs(const float (&acc)[R][M], int lane, int n0, int n_end, int N,
                                               uint16_t* __restrict__ y) {
-#if WUSH_GEMV_RS
     constexpr int V = pow2_ceil(R * M);
     if constexpr (V > 1) {
+        // recursive-halving reduce-scatter: about 2V VALU operations for V outputs
         float v[V];
 #pragma unroll
         for (int i = 0; i < V; ++i) v[i] = i < R * M ? acc[i / M][i % M] : 0.0f;
@@ -97,20 +95,9 @@ __device__ __forceinline__ void store_outputs(const float (&acc)[R][M], int lane
         const int r = idx / M, m = idx % M;
         if ((lane & (64 / V - 1)) == 0 && idx < R * M && n0 + r < n_end)
             y[(size_t)m * N + n0 + r] = f32_to_f16_bits(total);
-        return;
-    }
-#endif
-    float v[R][M];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < M; ++m) v[r][m] = wave_sum_dpp(acc[r][m]);
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int m = 0; m < M; ++m)
-                if (n0 + r < n_end) y[(size_t)m * N + n0 + r] = f32_to_f16_bits(v[r][m]);
+    } else {
+        const float total = wave_sum_dpp(acc[0][0]);
+        if (lane == 0 && n0 < n_end) y[n0] = f32_to_f16_bits(total);
     }
 }
 
@@ -286,43 +273,75 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
     }
 }
 
-template <int M, int R, int GPL>
-static void launch_gemv_t(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
-                          uint16_t* y, int N, int K, hipStream_t stream) {
+// Register-limited workgroups per CU of every kernel instance and the
+// device's LDS per CU and CU count, per device, filled by gemv_init_device
+// (the library's one-time set-up) before any launch.
+constexpr int kGemvGpl[3] = {0, 2, 4};
+struct GemvDeviceInfo {
+    int blocks_by_regs[8][3];                    // [M - 1][GPL index]
+    int lds_per_cu;
+    int cus;
+};
+static GemvDeviceInfo g_gemv_info[kMaxDevices];
+
+template <int M>
+constexpr int gemv_rows() {
+    return M == 1 ? WUSH_GEMV_R1 : M == 2 ? WUSH_GEMV_R2 : M <= 4 ? WUSH_GEMV_R4 : M <= 6 ? WUSH_GEMV_R8 : WUSH_GEMV_R78;
+}
+
+template <int M, int GI>
+static int gemv_query(GemvDeviceInfo& info) {
+    constexpr int R = gemv_rows<M>();
+    constexpr int GPL = kGemvGpl[GI];
+    int b = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, gemv_int4_kernel<M, R, GPL>,
+                                                                      64 * gemv_waves<M>(), 0);
+    if (e != hipSuccess) return (int)e;
+    info.blocks_by_regs[M - 1][GI] = b < 1 ? 1 : b;
+    if constexpr (GI < 2) return gemv_query<M, GI + 1>(info);
+    else if constexpr (M < 8) return gemv_query<M + 1, 0>(info);
+    else return 0;
+}
+
+int gemv_init_device(int dev) {
+    GemvDeviceInfo& info = g_gemv_info[dev];
+    if (hipDeviceGetAttribute(&info.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || info.cus < 1)
+        info.cus = 256;
+    if (hipDeviceGetAttribute(&info.lds_per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) !=
+            hipSuccess || info.lds_per_cu < 65536)
+        info.lds_per_cu = 65536;
+    return gemv_query<1, 0>(info);
+}
+
+template <int M, int GI>
+static void launch_gemv_t(const GemvDeviceInfo& info, const uint8_t* xq, const uint16_t* xs, const uint8_t* wq,
+                          const uint16_t* ws, uint16_t* y, int N, int K, hipStream_t stream) {
+    constexpr int R = gemv_rows<M>();
+    constexpr int GPL = kGemvGpl[GI];
     const int G = K / 32;
     const size_t smem = (size_t)M * (K / 2) + (size_t)M * G * sizeof(XsStage<M>);
     // Spread the rows evenly over the wavefronts that are resident at once
-    // (occupancy from the kernel's register and LDS use), so every CU
-    // finishes together.
+    // (workgroups per CU: the register limit and the LDS limit for this
+    // smem), so every CU finishes together.
     constexpr int kGemvWaves = gemv_waves<M>();
-    static int resident_waves = 0;
-    if (resident_waves == 0) {
-        int per_cu = 0;
-        int dev = 0, cus = 256;
-        if (hipGetDevice(&dev) == hipSuccess)
-            (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_int4_kernel<M, R, GPL>, 64 * kGemvWaves,
-                                                         smem) != hipSuccess || per_cu < 1)
-            per_cu = 2;
-        resident_waves = per_cu * kGemvWaves * cus;
-    }
-    int rows_per_wave = (N + resident_waves - 1) / resident_waves;
-    rows_per_wave = max(rows_per_wave, 1);
+    const int per_cu = max(1, min(info.blocks_by_regs[M - 1][GI], (int)(info.lds_per_cu / smem)));
+    const int resident_waves = per_cu * kGemvWaves * info.cus;
+    const int rows_per_wave = max((N + resident_waves - 1) / resident_waves, 1);
     const int blocks = (N + kGemvWaves * rows_per_wave - 1) / (kGemvWaves * rows_per_wave);
     gemv_int4_kernel<M, R, GPL><<<dim3(blocks), dim3(64 * kGemvWaves), smem, stream>>>(xq, xs, wq, ws, y, N, K,
                                                                                         rows_per_wave);
 }
 
-template <int M, int R>
-static void launch_gemv(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
-                        uint16_t* y, int N, int K, hipStream_t stream) {
+template <int M>
+static void launch_gemv(const GemvDeviceInfo& info, const uint8_t* xq, const uint16_t* xs, const uint8_t* wq,
+                        const uint16_t* ws, uint16_t* y, int N, int K, hipStream_t stream) {
     const int G = K / 32;
     if (G == 128)
-        launch_gemv_t<M, R, 2>(xq, xs, wq, ws, y, N, K, stream);
+        launch_gemv_t<M, 1>(info, xq, xs, wq, ws, y, N, K, stream);
     else if (G == 256)
-        launch_gemv_t<M, R, 4>(xq, xs, wq, ws, y, N, K, stream);
+        launch_gemv_t<M, 2>(info, xq, xs, wq, ws, y, N, K, stream);
     else
-        launch_gemv_t<M, R, 0>(xq, xs, wq, ws, y, N, K, stream);
+        launch_gemv_t<M, 0>(info, xq, xs, wq, ws, y, N, K, stream);
 }
 
 }  // namespace wush
@@ -338,16 +357,20 @@ extern "C" int wush_gemv_int4(const uint8_t* xq, const uint16_t* xs, const uint8
     WUSH_REQUIRE(((uintptr_t)xs & 1u) == 0 && ((uintptr_t)ws & 1u) == 0 && ((uintptr_t)y & 1u) == 0);
     // LDS holds M*K/2 code bytes + M*K/32 pairs of fp32 scale terms.
     WUSH_REQUIRE((size_t)M * (K / 2) + (size_t)M * (K / 32) * 8 <= 64 * 1024);
+    int dev = 0;
+    const int st = wush::device_setup(&dev);
+    if (st != 0) return st;
+    const wush::GemvDeviceInfo& info = wush::g_gemv_info[dev];
     const int n = (int)N, k = (int)K;
     switch (M) {
-        case 1: wush::launch_gemv<1, WUSH_GEMV_R1>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 2: wush::launch_gemv<2, WUSH_GEMV_R2>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 3: wush::launch_gemv<3, WUSH_GEMV_R4>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 4: wush::launch_gemv<4, WUSH_GEMV_R4>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 5: wush::launch_gemv<5, WUSH_GEMV_R8>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 6: wush::launch_gemv<6, WUSH_GEMV_R8>(xq, xs, wq, ws, y, n, k, stream); break;
-        case 7: wush::launch_gemv<7, WUSH_GEMV_R78>(xq, xs, wq, ws, y, n, k, stream); break;
-        default: wush::launch_gemv<8, WUSH_GEMV_R78>(xq, xs, wq, ws, y, n, k, stream); break;
+        case 1: wush::launch_gemv<1>(info, xq, xs, wq, ws, y, n, k, stream); break;
+        case 2: wush::launch_gemv<2>(info, xq, xs, wq, ws, y, n, k, stream); break;
+        case 3: wush::launch_gemv<3>(info, xq, xs, wq, ws, y, n, k, stream); break;
+        case 4: wush::launch_gemv<4>(info, xq, xs, wq, ws, y, n, k, stream); break;
+        case 5: wush::launch_gemv<5>(info, xq, xs, wq, ws, y, n, k, stream); break;
+        case 6: wush::launch_gemv<6>(info, xq, xs, wq, ws, y, n, k, stream); break;
+        case 7: wush::launch_gemv<7>(info, xq, xs, wq, ws, y, n, k, stream); break;
+        default: wush::launch_gemv<8>(info, xq, xs, wq, ws, y, n, k, stream); break;
     }
     return (int)hipGetLastError();
 }
