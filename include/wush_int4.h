@@ -102,6 +102,29 @@ int wush_gemm_s4(const uint8_t *xq, const uint16_t *xs, const uint8_t *wq, const
                  uint16_t *y, int64_t M, int64_t N, int64_t K,
                  void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Bytes of the static split-K scratch that wush_gemm_s4_noalloc uses: one
+ * array per device, held from the library's load until the process ends. */
+#define WUSH_GEMM_SCRATCH_BYTES (64u << 20)
+
+/* Status of wush_gemm_s4_noalloc when the shape's split-K plan needs more than
+ * WUSH_GEMM_SCRATCH_BYTES (wush_error_string explains it). */
+#define WUSH_ERROR_SCRATCH_TOO_SMALL 0x57550001
+
+/* wush_gemm_s4 that allocates nothing and takes no workspace: its split-K
+ * partials (if the plan splits K) go to the library's static scratch of
+ * WUSH_GEMM_SCRATCH_BYTES on the current device.  Same plan, kernels and
+ * results as wush_gemm_s4 given wush_gemm_s4_workspace_bytes(M, N, K) bytes of
+ * workspace; a shape whose plan needs more scratch than that returns
+ * WUSH_ERROR_SCRATCH_TOO_SMALL and launches nothing.  Nothing needs clearing
+ * between calls: every partial is written before it is summed.  All calls on
+ * one device share its scratch, so calls that overlap on one device (on
+ * different streams, or from different host threads without ordering) race.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture that must not call hipMalloc, tight
+ * serving loops, harnesses that forbid allocation). */
+int wush_gemm_s4_noalloc(const uint8_t *xq, const uint16_t *xs, const uint8_t *wq, const uint16_t *ws,
+                         uint16_t *y, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
 /* Self-test of the int8 MFMA operand layout the GEMM relies on:
  * c (8x8 int32) = a (8x32 int8, row-major) @ b (32x8 int8, row-major).
  * Replaces s4_atom_selftest (csrc/gemm_s4.cu:74-82). */

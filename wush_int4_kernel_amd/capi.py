@@ -24,6 +24,7 @@ SIGNATURES = {
     "wush_gemv_int4": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P], _I),
     "wush_gemm_s4_workspace_bytes": ([_I64, _I64, _I64], _SZ),
     "wush_gemm_s4": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P], _I),
+    "wush_gemm_s4_noalloc": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P], _I),
     "wush_mfma_selftest": ([_P, _P, _P, _P], _I),
     "wush_quant_int4_tensor_scale": ([_P, _P, _I64, _F, _P, _P], _I),
     "wush_gemm_s4_tensor_scale": ([_P, _P, _P, _I64, _I64, _I64, _F, _P, _P], _I),
@@ -78,6 +79,14 @@ def gemm_s4_workspace_bytes(M, N, K) -> int:
 def gemm_s4(xq, xs, wq, ws, y, M, N, K, workspace, workspace_bytes, stream) -> None:
     _check(load().wush_gemm_s4(xq, xs, wq, ws, y, M, N, K, workspace, workspace_bytes, stream),
            "wush_gemm_s4")
+
+
+GEMM_SCRATCH_BYTES = 64 << 20          # WUSH_GEMM_SCRATCH_BYTES
+ERROR_SCRATCH_TOO_SMALL = 0x57550001   # WUSH_ERROR_SCRATCH_TOO_SMALL
+
+
+def gemm_s4_noalloc(xq, xs, wq, ws, y, M, N, K, stream) -> None:
+    _check(load().wush_gemm_s4_noalloc(xq, xs, wq, ws, y, M, N, K, stream), "wush_gemm_s4_noalloc")
 
 
 def mfma_selftest(a, b, c, stream) -> None:

@@ -26,6 +26,7 @@
 // order (deterministic, graph-capturable, no atomics, no memset).
 #include "wush_device.h"
 #include "gemm_h16.h"
+#include "setup.h"
 #include "../../include/wush_int4.h"
 
 namespace wush {
@@ -922,6 +923,26 @@ int wush_gemm_s4(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const
     WUSH_REQUIRE(workspace == nullptr || ((uintptr_t)workspace & 3u) == 0);
     return wush::run_gemm<false>(xq, xs, wq, ws, y, M, N, K, workspace, workspace_bytes, 1.0f, nullptr,
                                  stream);
+}
+
+int wush_gemm_s4_noalloc(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
+                         uint16_t* y, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+    WUSH_REQUIRE(M >= 0 && N >= 0 && K > 0 && K % 32 == 0);
+    WUSH_REQUIRE(M <= 0x7fffffffLL && N <= 0x7fffffffLL && K <= 0x7fffffffLL);
+    if (M == 0 || N == 0) return (int)hipSuccess;
+    WUSH_REQUIRE(xq && xs && wq && ws && y);
+    WUSH_REQUIRE(((uintptr_t)xq & 15u) == 0 && ((uintptr_t)wq & 15u) == 0);
+    WUSH_REQUIRE(((uintptr_t)xs & 1u) == 0 && ((uintptr_t)ws & 1u) == 0 && ((uintptr_t)y & 1u) == 0);
+    // the plan wush_gemm_s4 runs with wush_gemm_s4_workspace_bytes(M, N, K)
+    // bytes of workspace; its split-K partials go to this device's scratch
+    const size_t need = wush_gemm_s4_workspace_bytes(M, N, K);
+    if (need > (size_t)WUSH_GEMM_SCRATCH_BYTES) return WUSH_ERROR_SCRATCH_TOO_SMALL;
+    int dev = 0;
+    const int st = wush::device_setup(&dev);
+    if (st != 0) return st;
+    void* scratch = need ? wush::scratch_address(dev) : nullptr;
+    if (need && scratch == nullptr) return (int)hipErrorInvalidSymbol;
+    return wush::run_gemm<false>(xq, xs, wq, ws, y, M, N, K, scratch, need, 1.0f, nullptr, stream);
 }
 
 int wush_gemm_s4_tensor_scale(const uint8_t* xq, const uint8_t* wq, uint16_t* y, int64_t M, int64_t N,

@@ -246,6 +246,9 @@ int wush_abi_version(void) { return WUSH_INT4_ABI_VERSION; }
 
 const char* wush_error_string(int status) {
     if (status == (int)hipErrorInvalidValue) return "wush_int4: invalid argument";
+    if (status == WUSH_ERROR_SCRATCH_TOO_SMALL)
+        return "wush_int4: the shape's split-K plan needs more than WUSH_GEMM_SCRATCH_BYTES of scratch "
+               "(call wush_gemm_s4 with a workspace instead)";
     return hipGetErrorString((hipError_t)status);
 }
 

@@ -16,6 +16,13 @@ namespace {
 std::once_flag g_once[kMaxDevices];
 int g_status[kMaxDevices];
 
+// Split-K scratch of wush_gemm_s4_noalloc: every device holds its own copy
+// from the library's load until the process ends.  Host code never uses the
+// array's name as an address (on the host it is a stand-in symbol): the
+// device address comes from hipGetSymbolAddress, once per device, below.
+static __device__ __align__(256) float scratch[WUSH_GEMM_SCRATCH_BYTES / sizeof(float)];
+void* g_scratch[kMaxDevices];
+
 }  // namespace
 
 int device_setup(int* dev) {
@@ -26,11 +33,19 @@ int device_setup(int* dev) {
     std::call_once(g_once[d], [d] {
         int st = gemm_h16_init_device();
         if (st == 0) st = gemv_init_device(d);
+        if (st == 0) {
+            void* p = nullptr;
+            st = (int)hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (st == 0 && p == nullptr) st = (int)hipErrorInvalidSymbol;
+            g_scratch[d] = st == 0 ? p : nullptr;
+        }
         g_status[d] = st;
     });
     *dev = d;
     return g_status[d];
 }
+
+void* scratch_address(int dev) { return dev >= 0 && dev < kMaxDevices ? g_scratch[dev] : nullptr; }
 
 }  // namespace wush
 
