@@ -17,7 +17,13 @@
  *     rounding ties, where a wrong last bit flips a code), and against v = h*sf
  *     scaled by 2^j (quotients near integers, half-integers at every binade);
  *   - 2^31 pseudo-random (v, sf) pairs over the whole exponent range.
- * q2 is compared with the division bit for bit, not only the code. */
+ * q2 is compared with the division bit for bit, not only the code.
+ *
+ * The one-fma form (wush_device.h, code8_fast) is checked on the same cases:
+ *     t = fma(v, r, 8), k = rint(t),
+ *     code = clamp(k, 1, 15) - 8 when |t - k| < 0.5 - 2^-17,
+ * otherwise the lane falls back to q2 above; its code must equal the
+ * division's wherever the band test passes. */
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -57,7 +63,18 @@ static int code_of_q(float q) {
     return (int)c - 8;
 }
 
+/* code8_fast: the code, or 99 when the lane would take the exact fallback */
+static int code_fast(float v, float r) {
+    float t = fmaf(v, r, 8.0f);
+    float k = rintf(t);
+    if (fabsf(t - k) >= 0.5f - 0x1p-17f) return 99;
+    if (k < 1.0f) k = 1.0f;
+    if (k > 15.0f) k = 15.0f;
+    return (int)k - 8;
+}
+
 static long bad = 0, checked = 0;
+static long bad_fast = 0, fallback = 0;
 
 static long bad_bits = 0;
 
@@ -65,9 +82,16 @@ static long bad_bits = 0;
  * bit for bit wherever quotient and remainders are normal numbers (|v| and
  * |v/sf| >= 2^-100; below that a remainder or the quotient can underflow, but
  * then |v/sf| < 2^-73 and both codes are 0). */
-static int check(float v, float sf, float r, long* nbad, long* nbits) {
+static int check(float v, float sf, float r, long* nbad, long* nbits, long* nfast, long* nfall) {
     if (!isfinite(v) || fabsf(v) >= 1.8e19f) return 0;
     float qd = v / sf, qf = quotient_fma(v, sf, r);
+    int cf = code_fast(v, r);
+    if (cf == 99) {
+        (*nfall)++;
+    } else if (cf != code_of_q(qd)) {
+        if (*nfast < 5) printf("one-fma code mismatch v=%a sf=%a division=%a\n", v, sf, qd);
+        (*nfast)++;
+    }
     if (code_of_q(qd) != code_of_q(qf)) {
         if (*nbad < 5) printf("code mismatch v=%a sf=%a division=%a fma=%a\n", v, sf, qd, qf);
         (*nbad)++;
@@ -87,7 +111,7 @@ static uint32_t next_u32(uint64_t* st) {
 
 int main(void) {
     /* ties and their neighbours, every bf16 scale */
-#pragma omp parallel for reduction(+ : bad, bad_bits, checked) schedule(dynamic, 64)
+#pragma omp parallel for reduction(+ : bad, bad_bits, checked, bad_fast, fallback) schedule(dynamic, 64)
     for (uint32_t sb = 0; sb < 0x7f80; ++sb) {
         float sf = bf16_value(sb);
         if (!(sf >= 1e-8f)) continue;
@@ -97,27 +121,28 @@ int main(void) {
             for (int j = -3; j <= 3; ++j) {
                 float b = ldexpf(base, j);
                 float up = b, dn = b;
-                checked += check(b, sf, r, &bad, &bad_bits);
+                checked += check(b, sf, r, &bad, &bad_bits, &bad_fast, &fallback);
                 for (int k = 0; k < 64; ++k) {
                     up = nextafterf(up, INFINITY);
                     dn = nextafterf(dn, -INFINITY);
-                    checked += check(up, sf, r, &bad, &bad_bits);
-                    checked += check(dn, sf, r, &bad, &bad_bits);
+                    checked += check(up, sf, r, &bad, &bad_bits, &bad_fast, &fallback);
+                    checked += check(dn, sf, r, &bad, &bad_bits, &bad_fast, &fallback);
                 }
             }
         }
     }
     /* pseudo-random pairs over the exponent range, 2^29 per run */
-#pragma omp parallel for reduction(+ : bad, bad_bits, checked) schedule(static)
+#pragma omp parallel for reduction(+ : bad, bad_bits, checked, bad_fast, fallback) schedule(static)
     for (int chunk = 0; chunk < 512; ++chunk) {
         uint64_t st = 0x9E3779B97F4A7C15ull ^ ((uint64_t)chunk * 0xD1B54A32D192ED03ull);
         for (long i = 0; i < (1L << 20); ++i) {
             uint32_t sb = 0x3280 + next_u32(&st) % (0x7f00 - 0x3280);  /* bf16 scales from ~1.5e-8 up */
             float sf = bf16_value(sb);
             float v = f_from_bits(next_u32(&st) & 0xdfffffffu);        /* exponent field < 192 */
-            checked += check(v, sf, 1.0f / sf, &bad, &bad_bits);
+            checked += check(v, sf, 1.0f / sf, &bad, &bad_bits, &bad_fast, &fallback);
         }
     }
-    printf("checked %ld (v, sf) pairs, code mismatches %ld, quotient mismatches %ld\n", checked, bad, bad_bits);
-    return (bad != 0 || bad_bits != 0);
+    printf("checked %ld (v, sf) pairs, code mismatches %ld, quotient mismatches %ld, "
+           "one-fma code mismatches %ld (fallbacks %ld)\n", checked, bad, bad_bits, bad_fast, fallback);
+    return (bad != 0 || bad_bits != 0 || bad_fast != 0);
 }

@@ -139,6 +139,40 @@ def test_quant_outliers_zeros_ties_overflow(capi):
     assert np.array_equal(q, qo) and np.array_equal(s, so)
 
 
+def test_quant_f32_near_ties(capi):
+    # fp32 codes come from one fma per element, t = RN(v * RN(1/sf) + 8), and a
+    # lane whose t lies within 2^-17 of a half-integer redoes its group with
+    # the correctly rounded quotient (wush_device.h, code8_fast).  Groups hold
+    # two anchors +-40 that dominate the variance, so the scale sf settles after
+    # a few rebuilds, and 30 values h*sf +- k ulps (h a half-integer, |k| <= 3):
+    # quotients at and next to rounding ties.  The second half of the groups
+    # keeps its values away from ties (the fast path alone).  Codes and scales
+    # must match the division bit for bit.
+    g = rng(1004)
+    n = 512
+    x = np.zeros((n, 32), np.float32)
+    x[:, 0], x[:, 1] = np.float32(40.0), np.float32(-40.0)
+    h = (g.integers(-5, 6, (n, 30)) * 0.5).astype(np.float32)
+    h[n // 2:] += g.uniform(-0.4, 0.4, (n // 2, 30)).astype(np.float32)
+    k = g.integers(-3, 4, (n, 30))
+    sf = np.full(n, 4.0, np.float32)
+    for _ in range(10):
+        v = (h * sf[:, None]).astype(np.float32)
+        for step in range(3):
+            v[k > step] = np.nextafter(v[k > step], np.float32(np.inf))
+            v[k < -step] = np.nextafter(v[k < -step], np.float32(-np.inf))
+        x[:, 2:] = v
+        _, so = oracle.quant(x, "f32")
+        sf = bf16_bits_to_f32(so.reshape(n))
+    q, s = run_quant(capi, x, "f32")
+    qo, so = oracle.quant(x, "f32")
+    assert np.array_equal(q, qo) and np.array_equal(s, so)
+    # the construction must put quotients in the fallback band
+    quot = x[:, 2:].astype(np.float64) / bf16_bits_to_f32(so.reshape(n)).astype(np.float64)[:, None]
+    near = np.abs(quot - np.floor(quot) - 0.5) < 2.0 ** -17
+    assert near[: n // 2].sum() > 1000 and near[n // 2:].sum() == 0
+
+
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_quant_other_dtypes(capi, dtype):
     g = rng(1002)
@@ -161,10 +195,14 @@ def test_fused_golden_fixture(capi):
     assert np.array_equal(q, fz["q"]) and np.array_equal(s, fz["s"])
 
 
-# the small-M kernel serves rows < 384, the rows kernel the rest
+# The small-M kernel serves launches of at most 16384 (row, block) pairs; the
+# rows kernel the rest, in its DPP form below 1536 wavefronts (ceil(rows/64)
+# x K/32) and its SGPR form from there.  Shapes cover all three, with partial
+# 64-row sets and block counts that leave a workgroup's 4 blocks partial.
 @pytest.mark.parametrize("rows,K", [(1, 32), (1, 4096), (3, 96), (8, 8192), (63, 256), (64, 256),
-                                    (65, 512), (130, 128), (256, 4096), (383, 256), (384, 256),
-                                    (385, 96), (1 << 16, 64)])
+                                    (65, 512), (130, 128), (383, 256), (384, 256), (385, 96),
+                                    (256, 4096), (200, 4096), (1000, 1056),
+                                    (1600, 2080), (1 << 16, 64)])
 def test_fused_random(capi, rows, K):
     g = rng(2000 + rows + K)
     xb = outlier_activations(g, rows, K)
@@ -175,14 +213,14 @@ def test_fused_random(capi, rows, K):
     assert np.array_equal(s, so)
 
 
-@pytest.mark.parametrize("rows", [5, 448])
+@pytest.mark.parametrize("rows", [5, 2500, 12300])
 def test_fused_extreme_operands_both_loops(capi, rows):
-    # The rows kernel (rows >= 384) runs an fma loop when every nonzero |x| of
-    # a wavefront's rows and |T| of its block lies in [2^-67, 2^51), and the
-    # mul-then-add loop otherwise.  Plant out-of-range values in some rows and
-    # T blocks (tiny, subnormal, huge, inf, NaN, at the range edges) so both
-    # loops and the vote between them run; every code and scale must still
-    # match the oracle bit for bit.
+    # The rows kernel (here 2500 rows: DPP form, 12300 rows: SGPR form) runs
+    # an fma loop when every nonzero |x| of a wavefront's rows and |T| of its
+    # block lies in [2^-67, 2^51), and the mul-then-add loop otherwise.  Plant
+    # out-of-range values in some rows and T blocks (tiny, subnormal, huge,
+    # inf, NaN, at the range edges) so both loops and the vote between them
+    # run; every code and scale must still match the oracle bit for bit.
     g = rng(2003 + rows)
     K = 256
     xb = outlier_activations(g, rows, K)

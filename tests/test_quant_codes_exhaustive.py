@@ -33,7 +33,9 @@ def test_fp32_quotients_equal_division_at_ties_and_random(tmp_path):
     # through RN(1/sf) and two fma corrections (wush_device.h, quotient_fma);
     # tests/native/quant_codes_fp32.c compares quotient and code with the IEEE
     # division at and next to every rounding tie for every bf16 scale, and on
-    # 2^29 random pairs (about 9e8 pairs, a few seconds on 8 cores).
+    # 2^29 random pairs (about 9e8 pairs, a few seconds on 8 cores).  The same
+    # pairs check the one-fma codes (wush_device.h, code8_fast) wherever their
+    # tie-band test lets them stand.
     exe = tmp_path / "quant_codes_fp32"
     src = os.path.join(HERE, "native", "quant_codes_fp32.c")
     subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-mfma", "-fopenmp", src, "-o", str(exe), "-lm"],
@@ -42,4 +44,4 @@ def test_fp32_quotients_equal_division_at_ties_and_random(tmp_path):
     env.setdefault("OMP_NUM_THREADS", str(min(8, os.cpu_count() or 1)))
     out = subprocess.run([str(exe)], capture_output=True, text=True, env=env, timeout=600)
     assert out.returncode == 0, out.stdout + out.stderr
-    assert "code mismatches 0, quotient mismatches 0" in out.stdout
+    assert "code mismatches 0, quotient mismatches 0, one-fma code mismatches 0" in out.stdout

@@ -87,10 +87,34 @@ __device__ __forceinline__ float code8_of_quotient(float q) {
     return __builtin_amdgcn_fmed3f(__builtin_rintf(q) + 8.0f, 1.0f, 15.0f);
 }
 
+// Code + 8 of v from t = RN(v*r + 8), one fma, with r = RN(1/sf); *far gets
+// the larger of itself and |t - rint(t)|.  For finite |v| < 1.8e19 and a
+// normal sf >= 1e-8, let q = v/sf (real).  If |q| <= 16, |t - (q + 8)| <= 2^-19
+// (r is within 2^-24 relative of 1/sf and t is rounded once, with an ulp of at
+// most 2^-19 below 32), and RN(q) is within 2^-21 of q.  So when
+// |t - rint(t)| < 0.5 - 2^-17 -- t more than 2^-17 away from every
+// half-integer -- q + 8 and RN(q) + 8 lie strictly inside the same unit
+// interval around k = rint(t), and clamp(rint(RN(q)), -7, 7) + 8 ==
+// clamp(k, 1, 15).  If |q| > 16 both sides clamp to the same end.  A lane
+// whose |t - rint(t)| reaches the band redoes its group with quotient_fma
+// (see quant_group32).  tests/native/quant_codes_fp32.c checks these codes
+// against the division at and next to every rounding tie.
+__device__ __forceinline__ float code8_fast(float v, float r, float* far) {
+    const float t = __builtin_fmaf(v, r, 8.0f);
+    const float k = __builtin_rintf(t);
+    *far = __builtin_fmaxf(*far, __builtin_fabsf(t - k));
+    return __builtin_amdgcn_fmed3f(k, 1.0f, 15.0f);
+}
+
+// |t - rint(t)| at or above this takes the exact quotient (code8_fast).
+constexpr float kTieBand = 0.5f - 0x1p-17f;
+
 // Quantize 32 fp32 values in registers: sequential sums, scale, 16 packed
 // bytes as 4 dwords (element 2k low nibble of byte k).
-// A group whose sum of squares is finite takes the division-free quotient;
-// one with an inf or NaN element (s2 not finite) keeps code_of's division.
+// A group whose sum of squares is finite takes the one-fma codes of
+// code8_fast, and a lane with a quotient near a rounding tie redoes its group
+// with the correctly rounded division-free quotient; one with an inf or NaN
+// element (s2 not finite) keeps code_of's division.
 __device__ __forceinline__ uint32_t quant_group32(const float (&v)[32], uint32_t (&w)[4]) {
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
@@ -112,6 +136,7 @@ __device__ __forceinline__ uint32_t quant_group32(const float (&v)[32], uint32_t
         return sb;
     }
     const float r = 1.0f / sf;
+    float far = 0.0f;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
         // even elements 8d+2k -> byte k of a, odd ones -> byte k of b; the
@@ -119,10 +144,23 @@ __device__ __forceinline__ uint32_t quant_group32(const float (&v)[32], uint32_t
         uint32_t a = 0, b = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            a = __builtin_amdgcn_cvt_pk_u8_f32(code8_of_quotient(quotient_fma(v[8 * d + 2 * k], sf, r)), k, a);
-            b = __builtin_amdgcn_cvt_pk_u8_f32(code8_of_quotient(quotient_fma(v[8 * d + 2 * k + 1], sf, r)), k, b);
+            a = __builtin_amdgcn_cvt_pk_u8_f32(code8_fast(v[8 * d + 2 * k], r, &far), k, a);
+            b = __builtin_amdgcn_cvt_pk_u8_f32(code8_fast(v[8 * d + 2 * k + 1], r, &far), k, b);
         }
         w[d] = (a ^ 0x08080808u) | ((b ^ 0x08080808u) << 4);
+    }
+    if (far >= kTieBand) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            uint32_t a = 0, b = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                a = __builtin_amdgcn_cvt_pk_u8_f32(code8_of_quotient(quotient_fma(v[8 * d + 2 * k], sf, r)), k, a);
+                b = __builtin_amdgcn_cvt_pk_u8_f32(code8_of_quotient(quotient_fma(v[8 * d + 2 * k + 1], sf, r)),
+                                                   k, b);
+            }
+            w[d] = (a ^ 0x08080808u) | ((b ^ 0x08080808u) << 4);
+        }
     }
     return sb;
 }
