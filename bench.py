@@ -403,6 +403,15 @@ def main():
         launch_product("gemm", 8, 24576, 4096, Wq8, Ws8)   # Qwen3-8B M=8 (K-split streaming GEMM, 8 rows)
         W3, S3 = _C.quant_int4((torch.randn(4096, 4096, generator=gdev, device=dev) * 0.02).to(torch.bfloat16))
         launch_product("gemm", 4096, 4096, 4096, W3, S3)  # 4096^3 prefill tiles
+        del W3, S3
+        # L70 M=4096 prefill and hipBLASLt bf16 at the same shape: the clock
+        # (GRBM_GUI_ACTIVE) and MFMA-busy comparison of the two
+        launch_product("gemm", 4096, N, K, wq, ws)
+        torch.backends.cuda.preferred_blas_library("hipblaslt")
+        Xp = activations_k(4096, K)
+        for _ in range(3):
+            torch.matmul(Xp, Wt.t())
+        del Xp
         torch.cuda.synchronize()
         src = torch.empty(256 << 20, dtype=torch.int16, device=dev)
         dst = torch.empty_like(src)
