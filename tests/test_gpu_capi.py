@@ -293,6 +293,43 @@ def test_gemv_matches_oracle(capi, M):
         assert rel_fro(y, ref) < FRO_TOL, (M, N, K, rel_fro(y, ref))
 
 
+def _random_code_operands(g, M, N, K, sx_exp=(124, 129), sw_exp=(120, 124)):
+    """Any nibbles (including -8) and bf16 scales with exponent fields in the
+    given ranges: the product does not care how the codes were quantized."""
+    xq = g.integers(0, 256, (M, K // 2), dtype=np.uint8)
+    wq = g.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    xs = ((g.integers(*sx_exp, (M, K // 32)) << 7) | g.integers(0, 128, (M, K // 32))).astype(np.uint16)
+    ws = ((g.integers(*sw_exp, (N, K // 32)) << 7) | g.integers(0, 128, (N, K // 32))).astype(np.uint16)
+    return xq, xs, wq, ws
+
+
+@pytest.mark.parametrize("M", [7, 8])
+def test_gemv_ksplit_matches_oracle(capi, M):
+    # M >= 7, K = 8192 (4 wavefronts per row range) and N > 32768 take the
+    # K-split GEMV; ragged N leaves a short last row range
+    g = rng(3050 + M)
+    N, K = 33000, 8192
+    xq, xs, wq, ws = _random_code_operands(g, M, N, K)
+    ref = oracle.gemm_f64(xq, xs, wq, ws)
+    y = run_gemm(capi, xq, xs, wq, ws, "gemv")
+    assert rel_fro(y, ref) < FRO_TOL, (M, rel_fro(y, ref))
+    y2 = run_gemm(capi, xq, xs, wq, ws, "gemm")
+    assert rel_fro(y, y2) < 1e-3
+
+
+def test_gemv_ksplit_scales_out_of_range(capi):
+    # activation scales of 2^61 (above the 2^60 limit of the conversion-free
+    # fold) send every wavefront to the conversion form, which rounds the same
+    # dot*sx*sw once; tiny weight scales keep the outputs in fp16's range
+    g = rng(3060)
+    M, N, K = 8, 33000, 8192
+    xq, xs, wq, ws = _random_code_operands(g, M, N, K, sx_exp=(188, 189), sw_exp=(64, 66))
+    ref = oracle.gemm_f64(xq, xs, wq, ws)
+    y = run_gemm(capi, xq, xs, wq, ws, "gemv")
+    assert np.isfinite(y).all()
+    assert rel_fro(y, ref) < FRO_TOL, rel_fro(y, ref)
+
+
 @pytest.mark.parametrize("M", [1, 4, 8])
 def test_gemv_int_exact(capi, M):
     g = rng(3100 + M)

@@ -16,7 +16,10 @@
 // the R x M partial sums go through a recursive-halving reduction (permlane
 // swaps and DPP, VALU only) that costs about two operations per output.  The
 // next chunk is requested before the current one is reduced, so each lane
-// keeps 2 x R x (K/2048) 16-byte loads outstanding.
+// keeps 2 x R x (K/2048) 16-byte loads outstanding.  At M = 7, 8 on long
+// rows (K % 2048 == 0, N > 32768) gemv_ks_kernel takes the product instead:
+// the K of a row is split over the wavefronts of a workgroup and every lane
+// keeps its group's activations in registers.
 #include "wush_device.h"
 #include "setup.h"
 #include "../../include/wush_int4.h"
@@ -273,12 +276,125 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
     }
 }
 
+// ------------------------------------------------ K-split GEMV, 5 <= M <= 8
+// For K % 2048 == 0: a workgroup of KS = K/2048 wavefronts streams a range of
+// weight rows; wavefront q takes groups 64q + lane, so each row is read as KS
+// loads of 1 KiB contiguous codes (and 128 B of scales), and every lane keeps
+// its one group's M activation codes and scale terms in registers for the
+// whole kernel -- no LDS activation reads per row (which cost ~12 us at L70
+// M=8 in the staged kernel above).  Rows go through a ring of KD 16-byte loads
+// per lane.  Per row, the M partial sums (one group per lane, so each is the
+// single rounding of dot*sx*sw) are reduced over the wavefront by recursive
+// halving into an LDS table [row][wavefront][m]; after the last row one
+// barrier, and the KS wavefront partials of each output are added in
+// wavefront order and stored.
+#ifndef WUSH_GEMV_KS_RING
+#define WUSH_GEMV_KS_RING 8
+#endif
+constexpr int kKsRing = WUSH_GEMV_KS_RING;        // rows in flight per wavefront
+#ifndef WUSH_GEMV_KS_MIN_M
+#define WUSH_GEMV_KS_MIN_M 7     // smallest M of the K-split kernel (9: off)
+#endif
+#ifndef WUSH_GEMV_KS_MIN_WAVES
+#define WUSH_GEMV_KS_MIN_WAVES 4 // ... and of K / 2048 (its wavefronts per workgroup)
+#endif
+#ifndef WUSH_GEMV_KS_MIN_N
+#define WUSH_GEMV_KS_MIN_N 32769 // ... and of N (K=8192 N=28672 M=8: 30.2 us against 27.9 staged)
+#endif
+constexpr int kGemvKsMinM = WUSH_GEMV_KS_MIN_M;
+constexpr size_t kGemvKsLds = 32 * 1024;          // bytes of the partial-sum table per workgroup
+// K % 2048 == 0 and at most 16 wavefronts per workgroup
+__host__ __device__ constexpr bool gemv_ks_shape(int64_t N, int64_t K) {
+    return N >= WUSH_GEMV_KS_MIN_N && K % 2048 == 0 && K / 2048 >= WUSH_GEMV_KS_MIN_WAVES && K / 2048 <= 16;
+}
+
+template <int M>
+__global__ __launch_bounds__(1024) void gemv_ks_kernel(const uint8_t* __restrict__ xq,
+                                                       const uint16_t* __restrict__ xs,
+                                                       const uint8_t* __restrict__ wq,
+                                                       const uint16_t* __restrict__ ws,
+                                                       uint16_t* __restrict__ y, int N, int K,
+                                                       int rows_per_wg) {
+    extern __shared__ __align__(16) float part[];           // [rows_per_wg][KS][M]
+    const int KS = blockDim.x >> 6;
+    const int G = K >> 5;
+    const int K2 = K >> 1;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int g = wave * 64 + lane;
+    const int n_begin = blockIdx.x * rows_per_wg;
+    const int n_end = min(N, n_begin + rows_per_wg);
+    const int cnt = n_end - n_begin;                 // >= 1: the grid covers N exactly
+
+    // this lane's group of every activation row; d' = kMagicBits + dot read
+    // as a float is kMagic + dot, so fma(d', sx, -kMagic*sx) = dot*sx exactly
+    uint4 xa[M];
+    float sx[M], nmx[M];
+    bool ok = true;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        xa[m] = *reinterpret_cast<const uint4*>(xq + (size_t)m * K2 + (size_t)g * 16);
+        sx[m] = bf16_to_f32(xs[(size_t)m * G + g]);
+        nmx[m] = -kMagic * sx[m];
+        ok = ok && scale_in_range(sx[m]);
+    }
+    const bool fast = __builtin_amdgcn_ballot_w64(!ok) == 0;
+
+    const uint8_t* wrow = wq + (size_t)n_begin * K2 + (size_t)g * 16;
+    const uint16_t* srow = ws + (size_t)n_begin * G + g;
+    uint4 rw[kKsRing];
+    uint32_t rs[kKsRing];
+    auto load = [&](int i, int d) {
+        const int r = min(i, cnt - 1);           // rows past the range re-read the last one (not stored)
+        rw[d] = load_nt16(wrow + (size_t)r * K2);
+        rs[d] = srow[(size_t)r * G];
+    };
+#pragma unroll
+    for (int d = 0; d < kKsRing; ++d) load(d, d);
+
+    constexpr int V = pow2_ceil(M);
+    const int idx = wave_rs_index<V>(lane);
+    const bool holder = (lane & (64 / V - 1)) == 0 && idx < M;
+    for (int i0 = 0; i0 < cnt; i0 += kKsRing) {
+#pragma unroll
+        for (int d = 0; d < kKsRing; ++d) {
+            const int i = i0 + d;
+            const float sw = bf16_to_f32(rs[d]);
+            float v[V];
+#pragma unroll
+            for (int m = 0; m < V; ++m) v[m] = 0.0f;
+            if (fast) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const int dot = dot32_s4(rw[d], xa[m], kMagicBits);
+                    v[m] = __builtin_fmaf(__int_as_float(dot), sx[m], nmx[m]) * sw;
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m) v[m] = (float)dot32_s4(rw[d], xa[m]) * (sx[m] * sw);
+            }
+            load(i + kKsRing, d);
+            const float total = wave_reduce_scatter<V>(v, lane);
+            if (holder && i < cnt) part[(i * KS + wave) * M + idx] = total;
+        }
+    }
+    __syncthreads();
+    // outputs of the range: add the KS partials in wavefront order
+    for (int o = threadIdx.x; o < M * cnt; o += blockDim.x) {
+        const int m = o / cnt, i = o - m * cnt;
+        float acc = part[(i * KS) * M + m];
+        for (int q = 1; q < KS; ++q) acc += part[(i * KS + q) * M + m];
+        y[(size_t)m * N + n_begin + i] = f32_to_f16_bits(acc);
+    }
+}
+
 // Register-limited workgroups per CU of every kernel instance and the
 // device's LDS per CU and CU count, per device, filled by gemv_init_device
 // (the library's one-time set-up) before any launch.
 constexpr int kGemvGpl[3] = {0, 2, 4};
 struct GemvDeviceInfo {
     int blocks_by_regs[8][3];                    // [M - 1][GPL index]
+    int ks_waves_per_cu[8];                      // gemv_ks_kernel<M>: register-limited wavefronts per CU
     int lds_per_cu;
     int cus;
 };
@@ -303,6 +419,18 @@ static int gemv_query(GemvDeviceInfo& info) {
     else return 0;
 }
 
+template <int M>
+static int gemv_ks_query(GemvDeviceInfo& info) {
+    if constexpr (M <= 8) {
+        int b = 0;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, gemv_ks_kernel<M>, 256, 0);
+        if (e != hipSuccess) return (int)e;
+        info.ks_waves_per_cu[M - 1] = b < 1 ? 4 : 4 * b;
+        return gemv_ks_query<M + 1>(info);
+    }
+    return 0;
+}
+
 int gemv_init_device(int dev) {
     GemvDeviceInfo& info = g_gemv_info[dev];
     if (hipDeviceGetAttribute(&info.cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || info.cus < 1)
@@ -310,7 +438,8 @@ int gemv_init_device(int dev) {
     if (hipDeviceGetAttribute(&info.lds_per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) !=
             hipSuccess || info.lds_per_cu < 65536)
         info.lds_per_cu = 65536;
-    return gemv_query<1, 0>(info);
+    const int st = gemv_query<1, 0>(info);
+    return st != 0 ? st : gemv_ks_query<kGemvKsMinM>(info);
 }
 
 template <int M, int GI>
@@ -332,10 +461,27 @@ static void launch_gemv_t(const GemvDeviceInfo& info, const uint8_t* xq, const u
                                                                                         rows_per_wave);
 }
 
+// K-split launch: KS = K/2048 wavefronts per workgroup, rows spread evenly
+// over the workgroups resident at once (registers and LDS).
+template <int M>
+static void launch_gemv_ks(const GemvDeviceInfo& info, const uint8_t* xq, const uint16_t* xs, const uint8_t* wq,
+                           const uint16_t* ws, uint16_t* y, int N, int K, hipStream_t stream) {
+    const int KS = K / 2048;
+    const int per_cu = max(1, info.ks_waves_per_cu[M - 1] / KS);
+    int rows = max(1, (N + per_cu * info.cus - 1) / (per_cu * info.cus));
+    while ((size_t)rows * KS * M * sizeof(float) > kGemvKsLds) rows = (rows + 1) / 2;
+    const int blocks = (N + rows - 1) / rows;
+    gemv_ks_kernel<M><<<dim3(blocks), dim3(64 * KS), (size_t)rows * KS * M * sizeof(float), stream>>>(
+        xq, xs, wq, ws, y, N, K, rows);
+}
+
 template <int M>
 static void launch_gemv(const GemvDeviceInfo& info, const uint8_t* xq, const uint16_t* xs, const uint8_t* wq,
                         const uint16_t* ws, uint16_t* y, int N, int K, hipStream_t stream) {
     const int G = K / 32;
+    if constexpr (M >= kGemvKsMinM) {
+        if (gemv_ks_shape(N, K)) return launch_gemv_ks<M>(info, xq, xs, wq, ws, y, N, K, stream);
+    }
     if (G == 128)
         launch_gemv_t<M, 1>(info, xq, xs, wq, ws, y, N, K, stream);
     else if (G == 256)
