@@ -215,9 +215,10 @@ def test_fused_random(capi, rows, K):
 
 @pytest.mark.parametrize("rows", [5, 2500, 12300])
 def test_fused_extreme_operands_both_loops(capi, rows):
-    # The rows kernel (here 2500 rows: DPP form, 12300 rows: SGPR form) runs
-    # an fma loop when every nonzero |x| of a wavefront's rows and |T| of its
-    # block lies in [2^-67, 2^51), and the mul-then-add loop otherwise.  Plant
+    # The rows kernel (here 2500 rows: DPP form, 12300 rows: SGPR form) and
+    # the small-M kernel (5 rows) run an fma loop when every nonzero |x| and
+    # |T| a wavefront multiplies lies in [2^-67, 2^51), and the mul-then-add
+    # loop otherwise.  Plant
     # out-of-range values in some rows and T blocks (tiny, subnormal, huge,
     # inf, NaN, at the range edges) so both loops and the vote between them
     # run; every code and scale must still match the oracle bit for bit.

@@ -24,7 +24,8 @@
 //  * small-M kernel (at most 16384 (row, block) pairs: decode, small batches):
 //    32 lanes per (row, block), two pairs per one-wavefront workgroup so a
 //    decode row spreads over K/64 CUs; lane j computes x'_j with T[c][j] read
-//    as 64 coalesced bytes and x broadcast from LDS; the group sums are then
+//    as 64 coalesced bytes and x broadcast from LDS (one fma per MAC when the
+//    wavefront's x and T are in range, as above); the group sums are then
 //    re-run in i-order by every lane from LDS (so they keep the sequential
 //    order) and lane pairs pack nibbles.
 #include <type_traits>
@@ -245,9 +246,10 @@ __global__ __launch_bounds__(64) void fused_tq_smallm_kernel(const uint16_t* __r
     const bool active = p < rows * C;
 
     uint4 tj[4];
-    tq_pair_load(x, t, K, p, active, j, xs[pl], tj);
+    const float x_own = tq_pair_load(x, t, K, p, active, j, xs[pl], tj);
+    const bool fast = __all(tq_pair_safe(tj, x_own));
     __syncthreads();
-    const float xj = tq_pair_matvec(xs[pl], tj);
+    const float xj = fast ? tq_pair_matvec<true>(xs[pl], tj) : tq_pair_matvec<false>(xs[pl], tj);
     xps[pl][j] = xj;
     __syncthreads();
     tq_pair_quant(xps[pl], xj, j, active, p, q, s);

@@ -52,30 +52,52 @@ __device__ __forceinline__ void load_bf16x32(const uint16_t* p, float (&v)[32]) 
 
 // Step 1: lane j stages x_j of pair p = r*C + c in LDS (xs_l, 32 floats) and
 // loads row j of T[c] as raw bf16 pairs (element 2d in the low half of word
-// d).  A barrier must follow before step 2.
-__device__ __forceinline__ void tq_pair_load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ t,
-                                             int64_t K, int64_t p, bool active, int j, float* xs_l,
-                                             uint4 (&tj)[4]) {
+// d); returns x_j.  A barrier must follow before step 2.
+__device__ __forceinline__ float tq_pair_load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ t,
+                                              int64_t K, int64_t p, bool active, int j, float* xs_l,
+                                              uint4 (&tj)[4]) {
     const int64_t C = K >> 5;
     const int64_t r = active ? p / C : 0;
     const int64_t c = active ? p % C : 0;
-    xs_l[j] = active ? bf16_to_f32(x[r * K + c * 32 + j]) : 0.0f;
+    const float xj = active ? bf16_to_f32(x[r * K + c * 32 + j]) : 0.0f;
+    xs_l[j] = xj;
     const uint4* row = reinterpret_cast<const uint4*>(t + c * 1024 + j * 32);
 #pragma unroll
     for (int k = 0; k < 4; ++k) tj[k] = active ? row[k] : make_uint4(0, 0, 0, 0);
+    return xj;
 }
 
 // Step 2: x'_j (T converted to fp32 as it is used).  The caller stores it
-// to LDS (xps_l[j]) and syncs.
+// to LDS (xps_l[j]) and syncs.  FAST (every x and T value of the wavefront
+// in BfRange's safe range, so each product is exact): one fma per MAC, bit
+// for bit the reference's acc + x*T; otherwise mul then add.
+template <bool FAST>
 __device__ __forceinline__ float tq_pair_matvec(const float* xs_l, const uint4 (&tj)[4]) {
     const uint32_t* u = &tj[0].x;
     float acc = 0.0f;
 #pragma unroll
     for (int d = 0; d < 16; ++d) {
-        acc = acc + xs_l[2 * d] * bf16_to_f32(u[d] & 0xffffu);
-        acc = acc + xs_l[2 * d + 1] * __uint_as_float(u[d] & 0xffff0000u);
+        const float t0 = bf16_to_f32(u[d] & 0xffffu), t1 = __uint_as_float(u[d] & 0xffff0000u);
+        if constexpr (FAST) {
+            acc = __builtin_fmaf(xs_l[2 * d], t0, acc);
+            acc = __builtin_fmaf(xs_l[2 * d + 1], t1, acc);
+        } else {
+            acc = acc + xs_l[2 * d] * t0;
+            acc = acc + xs_l[2 * d + 1] * t1;
+        }
     }
     return acc;
+}
+
+// Whether this lane's T row and staged x_j lie in BfRange's safe range.
+__device__ __forceinline__ bool tq_pair_safe(const uint4 (&tj)[4], float xj) {
+    BfRange rg;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        rg.add(tj[k].x); rg.add(tj[k].y); rg.add(tj[k].z); rg.add(tj[k].w);
+    }
+    rg.add(__float_as_uint(xj) >> 16);        // bf16 bits in the low half; the zero high half is ignored
+    return rg.safe();
 }
 
 // Step 3: the group's sums in i-order, its scale, lane j's code; even lanes
