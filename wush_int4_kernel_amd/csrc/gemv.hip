@@ -277,12 +277,14 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
 }
 
 // ------------------------------------------------ K-split GEMV, 5 <= M <= 8
-// For K % 2048 == 0: a workgroup of KS = K/2048 wavefronts streams a range of
-// weight rows; wavefront q takes groups 64q + lane, so each row is read as KS
-// loads of 1 KiB contiguous codes (and 128 B of scales), and every lane keeps
-// its one group's M activation codes and scale terms in registers for the
-// whole kernel -- no LDS activation reads per row (which cost ~12 us at L70
-// M=8 in the staged kernel above).  Rows go through a ring of KD 16-byte loads
+// For K % (2048 * GL) == 0: a workgroup of KS = K/(2048*GL) wavefronts streams
+// a range of weight rows; wavefront q takes groups 64(GL*q + t) + lane
+// (t < GL), so each row is read in loads of 1 KiB contiguous codes (and 128 B
+// of scales), and every lane keeps its GL groups' M activation codes and
+// scale terms in registers for the whole kernel -- no LDS activation reads per
+// row (which cost ~12 us at L70 M=8 in the staged kernel above).  GL = 1 is
+// built (GL = 2 halves the per-row reductions but needs 198 VGPRs at M=8 and
+// measured within 2%).  Rows go through a ring of KD 16-byte loads
 // per lane.  Per row, the M partial sums (one group per lane, so each is the
 // single rounding of dot*sx*sw) are reduced over the wavefront by recursive
 // halving into an LDS table [row][wavefront][m]; after the last row one
@@ -298,6 +300,10 @@ constexpr int kKsRing = WUSH_GEMV_KS_RING;        // rows in flight per wavefron
 #ifndef WUSH_GEMV_KS_MIN_WAVES
 #define WUSH_GEMV_KS_MIN_WAVES 4 // ... and of K / 2048 (its wavefronts per workgroup)
 #endif
+#ifndef WUSH_GEMV_KS_GL
+#define WUSH_GEMV_KS_GL 1        // groups per lane (K / (2048 * GL) wavefronts per workgroup)
+#endif
+constexpr int kKsGl = WUSH_GEMV_KS_GL;
 #ifndef WUSH_GEMV_KS_MIN_N
 #define WUSH_GEMV_KS_MIN_N 32769 // ... and of N (K=8192 N=28672 M=8: 30.2 us against 27.9 staged)
 #endif
@@ -305,11 +311,12 @@ constexpr int kGemvKsMinM = WUSH_GEMV_KS_MIN_M;
 constexpr size_t kGemvKsLds = 32 * 1024;          // bytes of the partial-sum table per workgroup
 // K % 2048 == 0 and at most 16 wavefronts per workgroup
 __host__ __device__ constexpr bool gemv_ks_shape(int64_t N, int64_t K) {
-    return N >= WUSH_GEMV_KS_MIN_N && K % 2048 == 0 && K / 2048 >= WUSH_GEMV_KS_MIN_WAVES && K / 2048 <= 16;
+    return N >= WUSH_GEMV_KS_MIN_N && K % (2048 * kKsGl) == 0 && K / 2048 >= WUSH_GEMV_KS_MIN_WAVES &&
+           K / (2048 * kKsGl) <= (kKsGl == 1 ? 16 : 4);
 }
 
-template <int M>
-__global__ __launch_bounds__(1024) void gemv_ks_kernel(const uint8_t* __restrict__ xq,
+template <int M, int GL>
+__global__ __launch_bounds__(GL == 1 ? 1024 : 256) void gemv_ks_kernel(const uint8_t* __restrict__ xq,
                                                        const uint16_t* __restrict__ xs,
                                                        const uint8_t* __restrict__ wq,
                                                        const uint16_t* __restrict__ ws,
@@ -321,33 +328,41 @@ __global__ __launch_bounds__(1024) void gemv_ks_kernel(const uint8_t* __restrict
     const int K2 = K >> 1;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
-    const int g = wave * 64 + lane;
     const int n_begin = blockIdx.x * rows_per_wg;
     const int n_end = min(N, n_begin + rows_per_wg);
     const int cnt = n_end - n_begin;                 // >= 1: the grid covers N exactly
 
-    // this lane's group of every activation row; d' = kMagicBits + dot read
-    // as a float is kMagic + dot, so fma(d', sx, -kMagic*sx) = dot*sx exactly
-    uint4 xa[M];
-    float sx[M], nmx[M];
+    // this lane's GL groups (64 * (GL * wave + t) + lane) of every activation
+    // row; d' = kMagicBits + dot read as a float is kMagic + dot, so
+    // fma(d', sx, -kMagic*sx) = dot*sx exactly
+    uint4 xa[GL][M];
+    float sx[GL][M], nmx[GL][M];
     bool ok = true;
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-        xa[m] = *reinterpret_cast<const uint4*>(xq + (size_t)m * K2 + (size_t)g * 16);
-        sx[m] = bf16_to_f32(xs[(size_t)m * G + g]);
-        nmx[m] = -kMagic * sx[m];
-        ok = ok && scale_in_range(sx[m]);
+    for (int t = 0; t < GL; ++t) {
+        const int g = 64 * (GL * wave + t) + lane;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            xa[t][m] = *reinterpret_cast<const uint4*>(xq + (size_t)m * K2 + (size_t)g * 16);
+            sx[t][m] = bf16_to_f32(xs[(size_t)m * G + g]);
+            nmx[t][m] = -kMagic * sx[t][m];
+            ok = ok && scale_in_range(sx[t][m]);
+        }
     }
     const bool fast = __builtin_amdgcn_ballot_w64(!ok) == 0;
 
-    const uint8_t* wrow = wq + (size_t)n_begin * K2 + (size_t)g * 16;
-    const uint16_t* srow = ws + (size_t)n_begin * G + g;
-    uint4 rw[kKsRing];
-    uint32_t rs[kKsRing];
+    const int g0 = 64 * GL * wave + lane;
+    const uint8_t* wrow = wq + (size_t)n_begin * K2 + (size_t)g0 * 16;
+    const uint16_t* srow = ws + (size_t)n_begin * G + g0;
+    uint4 rw[kKsRing][GL];
+    uint32_t rs[kKsRing][GL];
     auto load = [&](int i, int d) {
         const int r = min(i, cnt - 1);           // rows past the range re-read the last one (not stored)
-        rw[d] = load_nt16(wrow + (size_t)r * K2);
-        rs[d] = srow[(size_t)r * G];
+#pragma unroll
+        for (int t = 0; t < GL; ++t) {
+            rw[d][t] = load_nt16(wrow + (size_t)r * K2 + t * 1024);
+            rs[d][t] = srow[(size_t)r * G + t * 64];
+        }
     };
 #pragma unroll
     for (int d = 0; d < kKsRing; ++d) load(d, d);
@@ -359,19 +374,23 @@ __global__ __launch_bounds__(1024) void gemv_ks_kernel(const uint8_t* __restrict
 #pragma unroll
         for (int d = 0; d < kKsRing; ++d) {
             const int i = i0 + d;
-            const float sw = bf16_to_f32(rs[d]);
             float v[V];
 #pragma unroll
             for (int m = 0; m < V; ++m) v[m] = 0.0f;
-            if (fast) {
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const int dot = dot32_s4(rw[d], xa[m], kMagicBits);
-                    v[m] = __builtin_fmaf(__int_as_float(dot), sx[m], nmx[m]) * sw;
+            for (int t = 0; t < GL; ++t) {
+                const float sw = bf16_to_f32(rs[d][t]);
+                if (fast) {
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const int dot = dot32_s4(rw[d][t], xa[t][m], kMagicBits);
+                        v[m] = __builtin_fmaf(__builtin_fmaf(__int_as_float(dot), sx[t][m], nmx[t][m]), sw, v[m]);
+                    }
+                } else {
+#pragma unroll
+                    for (int m = 0; m < M; ++m)
+                        v[m] = __builtin_fmaf((float)dot32_s4(rw[d][t], xa[t][m]), sx[t][m] * sw, v[m]);
                 }
-            } else {
-#pragma unroll
-                for (int m = 0; m < M; ++m) v[m] = (float)dot32_s4(rw[d], xa[m]) * (sx[m] * sw);
             }
             load(i + kKsRing, d);
             const float total = wave_reduce_scatter<V>(v, lane);
@@ -394,7 +413,7 @@ __global__ __launch_bounds__(1024) void gemv_ks_kernel(const uint8_t* __restrict
 constexpr int kGemvGpl[3] = {0, 2, 4};
 struct GemvDeviceInfo {
     int blocks_by_regs[8][3];                    // [M - 1][GPL index]
-    int ks_waves_per_cu[8];                      // gemv_ks_kernel<M>: register-limited wavefronts per CU
+    int ks_waves_per_cu[8];                      // gemv_ks_kernel<M, GL>: register-limited wavefronts per CU
     int lds_per_cu;
     int cus;
 };
@@ -423,7 +442,7 @@ template <int M>
 static int gemv_ks_query(GemvDeviceInfo& info) {
     if constexpr (M <= 8) {
         int b = 0;
-        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, gemv_ks_kernel<M>, 256, 0);
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, gemv_ks_kernel<M, kKsGl>, 256, 0);
         if (e != hipSuccess) return (int)e;
         info.ks_waves_per_cu[M - 1] = b < 1 ? 4 : 4 * b;
         return gemv_ks_query<M + 1>(info);
@@ -461,17 +480,17 @@ static void launch_gemv_t(const GemvDeviceInfo& info, const uint8_t* xq, const u
                                                                                         rows_per_wave);
 }
 
-// K-split launch: KS = K/2048 wavefronts per workgroup, rows spread evenly
+// K-split launch: KS = K/(2048*GL) wavefronts per workgroup, rows spread evenly
 // over the workgroups resident at once (registers and LDS).
 template <int M>
 static void launch_gemv_ks(const GemvDeviceInfo& info, const uint8_t* xq, const uint16_t* xs, const uint8_t* wq,
                            const uint16_t* ws, uint16_t* y, int N, int K, hipStream_t stream) {
-    const int KS = K / 2048;
+    const int KS = K / (2048 * kKsGl);
     const int per_cu = max(1, info.ks_waves_per_cu[M - 1] / KS);
     int rows = max(1, (N + per_cu * info.cus - 1) / (per_cu * info.cus));
     while ((size_t)rows * KS * M * sizeof(float) > kGemvKsLds) rows = (rows + 1) / 2;
     const int blocks = (N + rows - 1) / rows;
-    gemv_ks_kernel<M><<<dim3(blocks), dim3(64 * KS), (size_t)rows * KS * M * sizeof(float), stream>>>(
+    gemv_ks_kernel<M, kKsGl><<<dim3(blocks), dim3(64 * KS), (size_t)rows * KS * M * sizeof(float), stream>>>(
         xq, xs, wq, ws, y, N, K, rows);
 }
 
