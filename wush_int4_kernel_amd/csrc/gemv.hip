@@ -57,6 +57,17 @@ constexpr int gemv_waves() { return M == 1 ? WUSH_GEMV_WAVES : M >= 7 ? WUSH_GEM
 #define WUSH_GEMV_R78 1         // ... at M = 7, 8 (L70 M=8: 48.3 us with 1 row, 51.4 with 2)
 #endif
 
+// dot32_s4 with the start value in an SGPR: the first v_dot8 reads it as its
+// third operand (the compiler would copy it to a VGPR per chain otherwise).
+__device__ __forceinline__ int dot32_s4_s(const uint4& a, const uint4& b, int init_s) {
+    int d;
+    asm("v_dot8_i32_i4 %0, %1, %2, %3" : "=v"(d) : "v"(a.x), "v"(b.x), "s"(init_s));
+    d = __builtin_amdgcn_sdot8((int)a.y, (int)b.y, d, false);
+    d = __builtin_amdgcn_sdot8((int)a.z, (int)b.z, d, false);
+    d = __builtin_amdgcn_sdot8((int)a.w, (int)b.w, d, false);
+    return d;
+}
+
 __device__ __forceinline__ int dot32_s4(const uint4& a, const uint4& b, int init = 0) {
     int d = __builtin_amdgcn_sdot8((int)a.x, (int)b.x, init, false);
     d = __builtin_amdgcn_sdot8((int)a.y, (int)b.y, d, false);
@@ -181,6 +192,8 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
         };
         Chunk cur, nxt;
         if (n_begin < n_end) load(n_begin, cur);
+        int magic;
+        asm("s_mov_b32 %0, %1" : "=s"(magic) : "n"(kMagicBits));   // kMagicBits in an SGPR (see dot32_s4_s)
 
         const bool x_in_range = stage_activations<M>(xq, xs, xq_l, xs_l, G);
 
@@ -210,7 +223,7 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
                         const float2 sx2 = xs_l[m * G + g];
 #pragma unroll
                         for (int r = 0; r < R; ++r) {
-                            const int d = dot32_s4(cur.w[r][t], xv, kMagicBits);
+                            const int d = dot32_s4_s(cur.w[r][t], xv, magic);
                             const float v = __builtin_fmaf(__int_as_float(d), sx2.x, sx2.y);
                             acc[r][m] = __builtin_fmaf(v, bf16_to_f32(cur.s[r][t]), acc[r][m]);
                         }
@@ -284,12 +297,16 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
 // scale terms in registers for the whole kernel -- no LDS activation reads per
 // row (which cost ~12 us at L70 M=8 in the staged kernel above).  GL = 1 is
 // built (GL = 2 halves the per-row reductions but needs 198 VGPRs at M=8 and
-// measured within 2%).  Rows go through a ring of KD 16-byte loads
-// per lane.  Per row, the M partial sums (one group per lane, so each is the
-// single rounding of dot*sx*sw) are reduced over the wavefront by recursive
-// halving into an LDS table [row][wavefront][m]; after the last row one
-// barrier, and the KS wavefront partials of each output are added in
-// wavefront order and stored.
+// measured within 2%).  Rows go through a ring of kKsRing 16-byte loads per
+// lane, addressed as a wave-uniform row base (SGPRs) plus the lane's 32-bit
+// offset, and the first ring is requested before the activations.  Per row,
+// the M partial sums (one group per lane, so each is the single rounding of
+// dot*sx*sw) are reduced over the wavefront by recursive halving into an LDS
+// table [row][wavefront][m]; after the last row one barrier, and the KS
+// wavefront partials of each output are added in wavefront order and stored.
+// A row costs 71 VALU instructions at M=8 (32 v_dot8, 16 fma, 23 for the
+// reduction and the row's scale; no per-chain v_mov of the start value and no
+// per-row address arithmetic: L70 M=8 46.9 against 50.2 us before).
 #ifndef WUSH_GEMV_KS_RING
 #define WUSH_GEMV_KS_RING 8
 #endif
@@ -315,6 +332,20 @@ __host__ __device__ constexpr bool gemv_ks_shape(int64_t N, int64_t K) {
            K / (2048 * kKsGl) <= (kKsGl == 1 ? 16 : 4);
 }
 
+// The pointer as a wave-uniform (SGPR) global-memory pointer: p must be the
+// same in every lane.  Loads from it plus a 32-bit lane offset then use the
+// scalar-base address form with no per-lane 64-bit arithmetic.
+template <typename T>
+using global_cptr = const __attribute__((address_space(1))) T*;
+
+template <typename T>
+__device__ __forceinline__ global_cptr<T> uniform_ptr(const T* p) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return reinterpret_cast<global_cptr<T>>(((uint64_t)hi << 32) | lo);
+}
+
 template <int M, int GL>
 __global__ __launch_bounds__(GL == 1 ? 1024 : 256) void gemv_ks_kernel(const uint8_t* __restrict__ xq,
                                                        const uint16_t* __restrict__ xs,
@@ -331,6 +362,33 @@ __global__ __launch_bounds__(GL == 1 ? 1024 : 256) void gemv_ks_kernel(const uin
     const int n_begin = blockIdx.x * rows_per_wg;
     const int n_end = min(N, n_begin + rows_per_wg);
     const int cnt = n_end - n_begin;                 // >= 1: the grid covers N exactly
+
+    // Row r of the range: a wave-uniform base (SGPR arithmetic per row) plus
+    // the lane's 32-bit offset, so a row costs no VALU address arithmetic.
+    const uint8_t* wbase = wq + (size_t)n_begin * K2 + (size_t)(64 * GL * wave) * 16;
+    const uint16_t* sbase = ws + (size_t)n_begin * G + 64 * GL * wave;
+    const uint32_t woff = (uint32_t)lane * 16u;
+    uint4 rw[kKsRing][GL];
+    uint32_t rs[kKsRing][GL];
+    auto load = [&](int i, int d) {
+        const int r = min(i, cnt - 1);           // rows past the range re-read the last one (not stored)
+#pragma unroll
+        for (int t = 0; t < GL; ++t) {
+            uint32_t wo = woff;
+            asm("" : "+v"(wo));                  // keeps the 32-bit lane offset form (no hoisted 64-bit add)
+            const global_cptr<u32x4> wp =
+                reinterpret_cast<global_cptr<u32x4>>(uniform_ptr(wbase + ((size_t)r * K2 + t * 1024)) + wo);
+            const u32x4 wv = __builtin_nontemporal_load(wp);
+            rw[d][t] = make_uint4(wv.x, wv.y, wv.z, wv.w);
+            rs[d][t] = uniform_ptr(sbase + ((size_t)r * G + t * 64))[(uint32_t)lane];
+        }
+    };
+    // the first rows are requested before the activations: weights do not
+    // depend on them, and the range check below waits for the scales
+#pragma unroll
+    for (int d = 0; d < kKsRing; ++d) load(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+
 
     // this lane's GL groups (64 * (GL * wave + t) + lane) of every activation
     // row; d' = kMagicBits + dot read as a float is kMagic + dot, so
@@ -351,50 +409,59 @@ __global__ __launch_bounds__(GL == 1 ? 1024 : 256) void gemv_ks_kernel(const uin
     }
     const bool fast = __builtin_amdgcn_ballot_w64(!ok) == 0;
 
-    const int g0 = 64 * GL * wave + lane;
-    const uint8_t* wrow = wq + (size_t)n_begin * K2 + (size_t)g0 * 16;
-    const uint16_t* srow = ws + (size_t)n_begin * G + g0;
-    uint4 rw[kKsRing][GL];
-    uint32_t rs[kKsRing][GL];
-    auto load = [&](int i, int d) {
-        const int r = min(i, cnt - 1);           // rows past the range re-read the last one (not stored)
-#pragma unroll
-        for (int t = 0; t < GL; ++t) {
-            rw[d][t] = load_nt16(wrow + (size_t)r * K2 + t * 1024);
-            rs[d][t] = srow[(size_t)r * G + t * 64];
-        }
-    };
-#pragma unroll
-    for (int d = 0; d < kKsRing; ++d) load(d, d);
-
     constexpr int V = pow2_ceil(M);
     const int idx = wave_rs_index<V>(lane);
     const bool holder = (lane & (64 / V - 1)) == 0 && idx < M;
-    for (int i0 = 0; i0 < cnt; i0 += kKsRing) {
+    // The magic start value as a wave-uniform operand: the first v_dot8 of
+    // each chain reads it from an SGPR instead of a per-row v_mov.
+    int magic;
+    asm("s_mov_b32 %0, %1" : "=s"(magic) : "n"(kMagicBits));   // kMagicBits in an SGPR (see dot32_s4_s)
+    if (fast) {
+        for (int i0 = 0; i0 < cnt; i0 += kKsRing) {
 #pragma unroll
-        for (int d = 0; d < kKsRing; ++d) {
-            const int i = i0 + d;
+            for (int d = 0; d < kKsRing; ++d) {
+                const int i = i0 + d;
+                float v[V];
+#pragma unroll
+                for (int m = 0; m < V; ++m) v[m] = 0.0f;
+#pragma unroll
+                for (int t = 0; t < GL; ++t) {
+                    const float sw = bf16_to_f32(rs[d][t]);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const int dot = dot32_s4_s(rw[d][t], xa[t][m], magic);
+                        v[m] = __builtin_fmaf(__builtin_fmaf(__int_as_float(dot), sx[t][m], nmx[t][m]), sw, v[m]);
+                    }
+                }
+                load(i + kKsRing, d);
+                const float total = wave_reduce_scatter<V>(v, lane);
+                if (holder && i < cnt) part[(i * KS + wave) * M + idx] = total;
+            }
+        }
+    } else {
+        // A scale outside the conversion-free range (rare): fma((float)dot,
+        // sx*sw, .), one row at a time with its own loads, so this form adds
+        // nothing to the register budget of the one above.  The prefetched
+        // ring is only waited for here (which keeps its loads ahead of the
+        // activation range check on both paths).
+#pragma unroll
+        for (int d = 0; d < kKsRing; ++d)
+#pragma unroll
+            for (int t = 0; t < GL; ++t) asm volatile("" ::"v"(rw[d][t].x), "v"(rs[d][t]));
+        for (int i = 0; i < cnt; ++i) {
             float v[V];
 #pragma unroll
             for (int m = 0; m < V; ++m) v[m] = 0.0f;
 #pragma unroll
             for (int t = 0; t < GL; ++t) {
-                const float sw = bf16_to_f32(rs[d][t]);
-                if (fast) {
+                const uint4 wv = load_nt16(wbase + ((size_t)i * K2 + t * 1024) + woff);
+                const float sw = bf16_to_f32(sbase[((size_t)i * G + t * 64) + (uint32_t)lane]);
 #pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        const int dot = dot32_s4(rw[d][t], xa[t][m], kMagicBits);
-                        v[m] = __builtin_fmaf(__builtin_fmaf(__int_as_float(dot), sx[t][m], nmx[t][m]), sw, v[m]);
-                    }
-                } else {
-#pragma unroll
-                    for (int m = 0; m < M; ++m)
-                        v[m] = __builtin_fmaf((float)dot32_s4(rw[d][t], xa[t][m]), sx[t][m] * sw, v[m]);
-                }
+                for (int m = 0; m < M; ++m)
+                    v[m] = __builtin_fmaf((float)dot32_s4(wv, xa[t][m]), sx[t][m] * sw, v[m]);
             }
-            load(i + kKsRing, d);
             const float total = wave_reduce_scatter<V>(v, lane);
-            if (holder && i < cnt) part[(i * KS + wave) * M + idx] = total;
+            if (holder) part[(i * KS + wave) * M + idx] = total;
         }
     }
     __syncthreads();
