@@ -133,6 +133,20 @@ template <int M> using XsStage = typename XsStageT<M>::type;
 __device__ __forceinline__ float xs_at(const float* xs_l, int i) { return xs_l[i]; }
 __device__ __forceinline__ float xs_at(const float2* xs_l, int i) { return xs_l[i].x; }
 
+// The pointer as a wave-uniform (SGPR) global-memory pointer: p must be the
+// same in every lane.  Loads from it plus a 32-bit lane offset then use the
+// scalar-base address form with no per-lane 64-bit arithmetic.
+template <typename T>
+using global_cptr = const __attribute__((address_space(1))) T*;
+
+template <typename T>
+__device__ __forceinline__ global_cptr<T> uniform_ptr(const T* p) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return reinterpret_cast<global_cptr<T>>(((uint64_t)hi << 32) | lo);
+}
+
 // Stage the activation codes and scales in LDS; for M >= 2 returns whether
 // every sx of the block is in range (block-uniform).
 template <int M>
@@ -169,7 +183,7 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
     uint4* xq_l = reinterpret_cast<uint4*>(smem);                       // [M][G] x 16 B
     XS* xs_l = reinterpret_cast<XS*>(smem + (size_t)M * K2);            // [M][G]
 
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int n_begin = (blockIdx.x * gemv_waves<M>() + wave) * rows_per_wave;
     const int n_step = R;
@@ -181,12 +195,16 @@ __global__ __launch_bounds__(64 * gemv_waves<M>()) void gemv_int4_kernel(const u
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int n = max(0, min(n0 + r, n_end - 1));   // clamp: duplicate rows are never stored
-                const uint8_t* wrow = wq + (size_t)n * K2;
-                const uint16_t* srow = ws + (size_t)n * G;
+                // wave-uniform row base plus the lane's 32-bit offset
+                const global_cptr<uint8_t> wrow = uniform_ptr(wq + (size_t)n * K2);
+                const global_cptr<uint16_t> srow = uniform_ptr(ws + (size_t)n * G);
 #pragma unroll
                 for (int t = 0; t < GPL; ++t) {
-                    c.w[r][t] = load_nt16(wrow + (size_t)(lane + 64 * t) * 16);
-                    c.s[r][t] = srow[lane + 64 * t];
+                    uint32_t wo = (uint32_t)(lane + 64 * t) * 16u;
+                    asm("" : "+v"(wo));          // keeps the 32-bit lane offset form
+                    const u32x4 wv = __builtin_nontemporal_load(reinterpret_cast<global_cptr<u32x4>>(wrow + wo));
+                    c.w[r][t] = make_uint4(wv.x, wv.y, wv.z, wv.w);
+                    c.s[r][t] = srow[(uint32_t)(lane + 64 * t)];
                 }
             }
         };
@@ -330,20 +348,6 @@ constexpr size_t kGemvKsLds = 32 * 1024;          // bytes of the partial-sum ta
 __host__ __device__ constexpr bool gemv_ks_shape(int64_t N, int64_t K) {
     return N >= WUSH_GEMV_KS_MIN_N && K % (2048 * kKsGl) == 0 && K / 2048 >= WUSH_GEMV_KS_MIN_WAVES &&
            K / (2048 * kKsGl) <= (kKsGl == 1 ? 16 : 4);
-}
-
-// The pointer as a wave-uniform (SGPR) global-memory pointer: p must be the
-// same in every lane.  Loads from it plus a 32-bit lane offset then use the
-// scalar-base address form with no per-lane 64-bit arithmetic.
-template <typename T>
-using global_cptr = const __attribute__((address_space(1))) T*;
-
-template <typename T>
-__device__ __forceinline__ global_cptr<T> uniform_ptr(const T* p) {
-    const uint64_t a = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-    return reinterpret_cast<global_cptr<T>>(((uint64_t)hi << 32) | lo);
 }
 
 template <int M, int GL>
