@@ -77,7 +77,10 @@ int wush_fused_tq(const uint16_t *x, const uint16_t *t, uint8_t *q, uint16_t *s,
 
 /* Decode GEMV for 1 <= M <= 8: y[m][n] = sum_g sx[m][g]*sw[n][g]*D[m][n][g]
  * with D the exact int32 dot of group g.  xq: M*K/2; xs: M*K/32; wq: N*K/2;
- * ws: N*K/32; y: M*N fp16.
+ * ws: N*K/32; y: M*N fp16.  The activations must fit 64 KiB of LDS
+ * (M*K/2 + M*K/4 bytes), except at M = 7, 8 with K a multiple of 2048 in
+ * [8192, 32768] and N > 32768, which keep them in registers; other shapes
+ * return hipErrorInvalidValue (wush_gemm_s4 takes any shape).
  * Replaces w4a4_gemv (csrc/gemv_int4.cu:191-223, M == 1) and w4a4_gemv_multi
  * (csrc/gemv_int4.cu:145-189, M <= 8). */
 int wush_gemv_int4(const uint8_t *xq, const uint16_t *xs, const uint8_t *wq, const uint16_t *ws,

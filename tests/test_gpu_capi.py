@@ -331,6 +331,33 @@ def test_gemv_ksplit_scales_out_of_range(capi):
     assert rel_fro(y, ref) < FRO_TOL, rel_fro(y, ref)
 
 
+@pytest.mark.parametrize("K", [16384, 32768])
+def test_gemv_ksplit_more_wavefronts(capi, K):
+    # 8 and 16 wavefronts per row range (the largest K-split workgroup)
+    g = rng(3070 + K // 16384)
+    M, N = 8, 32800
+    xq, xs, wq, ws = _random_code_operands(g, M, N, K)
+    ref = oracle.gemm_f64(xq, xs, wq, ws)
+    y = run_gemm(capi, xq, xs, wq, ws, "gemv")
+    assert rel_fro(y, ref) < FRO_TOL, (K, rel_fro(y, ref))
+
+
+def test_gemv_ksplit_mixed_forms(capi):
+    # only wavefront 1's groups (64..127) carry activation scales above 2^60:
+    # that wavefront takes the conversion form, the other three the
+    # conversion-free one, and their partials meet in one sum per output
+    g = rng(3080)
+    M, N, K = 8, 33000, 8192
+    xq, xs, wq, ws = _random_code_operands(g, M, N, K, sw_exp=(64, 66))
+    xs[:, :64] = (xs[:, :64] & 0x7F) | (180 << 7)          # 2^53: in range
+    xs[:, 64:128] = (xs[:, 64:128] & 0x7F) | (188 << 7)    # 2^61: out of range
+    xs[:, 128:] = (xs[:, 128:] & 0x7F) | (180 << 7)
+    ref = oracle.gemm_f64(xq, xs, wq, ws)
+    y = run_gemm(capi, xq, xs, wq, ws, "gemv")
+    assert np.isfinite(y).all()
+    assert rel_fro(y, ref) < FRO_TOL, rel_fro(y, ref)
+
+
 @pytest.mark.parametrize("M", [1, 4, 8])
 def test_gemv_int_exact(capi, M):
     g = rng(3100 + M)

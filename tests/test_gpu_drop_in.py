@@ -260,6 +260,28 @@ def test_decode_ops_route_to_either_kernel(C, M):
         assert rel_fro(f16_tensor_f64(y1[:, cols]), ref) < 2e-3, (M, N, K)
 
 
+@pytest.mark.parametrize("M", [6, 7, 8])
+def test_decode_ops_ksplit_large_k(C, M):
+    # K = 16384, N > 32768: at M = 7, 8 both ops run the GEMV's K-split kernel
+    # (activations in registers, no LDS staging limit), at M = 6 the GEMM
+    # (the staged GEMV would need 72 KiB of LDS); random codes and scales
+    import torch
+    g = rng(90 + M)
+    N, K = 32800, 16384
+    wq = torch.from_numpy(g.integers(0, 256, (N, K // 2), dtype=np.uint8)).cuda()
+    ws = torch.from_numpy(((g.integers(118, 122, (N, K // 32)) << 7) | g.integers(0, 128, (N, K // 32)))
+                          .astype(np.int16)).cuda().view(torch.bfloat16)
+    xq = torch.from_numpy(g.integers(0, 256, (M, K // 2), dtype=np.uint8)).cuda()
+    xs = torch.from_numpy(((g.integers(124, 128, (M, K // 32)) << 7) | g.integers(0, 128, (M, K // 32)))
+                          .astype(np.int16)).cuda().view(torch.bfloat16)
+    cols = torch.from_numpy(np.sort(g.choice(N, size=512, replace=False))).cuda()
+    ref = oracle.gemm_f64(xq.cpu().numpy(), bf16_tensor_bits(xs), wq[cols].cpu().numpy(), bf16_tensor_bits(ws[cols]))
+    y1 = C.w4a4_gemm_s4(xq, xs, wq, ws)
+    y2 = C.w4a4_gemv_multi(xq, xs, wq, ws)
+    assert torch.equal(y1, y2), M
+    assert rel_fro(f16_tensor_f64(y1[:, cols]), ref) < 2e-3, M
+
+
 def test_rtn_int4_module_on_gpu(C):
     # my_int4.rtn_int4 (reference my_int4/rtn_int4.py:33-75): quant_int4 is
     # the bit-exact kernel, dequant_int4 decodes like the oracle, and

@@ -591,8 +591,10 @@ extern "C" int wush_gemv_int4(const uint8_t* xq, const uint16_t* xs, const uint8
     WUSH_REQUIRE(xq && xs && wq && ws && y);
     WUSH_REQUIRE(((uintptr_t)xq & 15u) == 0 && ((uintptr_t)wq & 15u) == 0);
     WUSH_REQUIRE(((uintptr_t)xs & 1u) == 0 && ((uintptr_t)ws & 1u) == 0 && ((uintptr_t)y & 1u) == 0);
-    // LDS holds M*K/2 code bytes + M*K/32 pairs of fp32 scale terms.
-    WUSH_REQUIRE((size_t)M * (K / 2) + (size_t)M * (K / 32) * 8 <= 64 * 1024);
+    // The staged kernel's LDS holds M*K/2 code bytes + M*K/32 pairs of fp32
+    // scale terms; the K-split kernel (M >= 7 on its shapes) stages nothing.
+    const bool ksplit = M >= wush::kGemvKsMinM && wush::gemv_ks_shape(N, K);
+    WUSH_REQUIRE(ksplit || (size_t)M * (K / 2) + (size_t)M * (K / 32) * 8 <= 64 * 1024);
     int dev = 0;
     const int st = wush::device_setup(&dev);
     if (st != 0) return st;
