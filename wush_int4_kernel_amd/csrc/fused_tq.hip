@@ -22,8 +22,9 @@
 //       hidden): vector loads, 16 pairs per VGPR converted on the VALU, every
 //       MAC reads its T value from another lane through DPP row_newbcast.
 //  * small-M kernel (at most 16384 (row, block) pairs: decode, small batches):
-//    32 lanes per (row, block), two pairs per one-wavefront workgroup so a
-//    decode row spreads over K/64 CUs; lane j computes x'_j with T[c][j] read
+//    32 lanes per (row, block), two adjacent blocks of one row per
+//    one-wavefront workgroup (grid: block pairs x rows) so a decode row
+//    spreads over K/64 CUs; lane j computes x'_j with T[c][j] read
 //    as 64 coalesced bytes and x broadcast from LDS (one fma per MAC when the
 //    wavefront's x and T are in range, as above); the group sums are then
 //    re-run in i-order by every lane from LDS (so they keep the sequential
@@ -237,16 +238,20 @@ __global__ __launch_bounds__(64) void fused_tq_smallm_kernel(const uint16_t* __r
                                                               uint8_t* __restrict__ q,
                                                               uint16_t* __restrict__ s,
                                                               int64_t rows, int64_t K) {
-    __shared__ float xs[kPairsPerWg][32];
-    __shared__ float xps[kPairsPerWg][32];
+    __shared__ __align__(16) float xs[kPairsPerWg][32];
+    __shared__ __align__(16) float xps[kPairsPerWg][32];
     const int pl = threadIdx.x >> 5;             // pair within the workgroup
     const int j = threadIdx.x & 31;              // output index within the block
+    // grid (ceil(C / 2), rows): the two pairs of a workgroup are blocks c,
+    // c + 1 of one row (no division for the pair's row and block)
     const int64_t C = K >> 5;
-    const int64_t p = (int64_t)blockIdx.x * kPairsPerWg + pl;
-    const bool active = p < rows * C;
+    const int64_t r = blockIdx.y;
+    const int64_t c = (int64_t)blockIdx.x * kPairsPerWg + pl;
+    const bool active = c < C;
+    const int64_t p = r * C + c;
 
     uint4 tj[4];
-    const float x_own = tq_pair_load(x, t, K, p, active, j, xs[pl], tj);
+    const float x_own = tq_pair_load(x, t, K, r, c, active, j, xs[pl], tj);
     const bool fast = __all(tq_pair_safe(tj, x_own));
     __syncthreads();
     const float xj = fast ? tq_pair_matvec<true>(xs[pl], tj) : tq_pair_matvec<false>(xs[pl], tj);
@@ -279,9 +284,9 @@ extern "C" int wush_fused_tq(const uint16_t* x, const uint16_t* t, uint8_t* q, u
                  ((uintptr_t)q & 15u) == 0 && ((uintptr_t)s & 1u) == 0);
     const int64_t C = K / 32;
     if (rows * C <= WUSH_TQ_SMALLM_PAIRS) {
-        const int64_t blocks = (rows * C + wush::kPairsPerWg - 1) / wush::kPairsPerWg;
-        WUSH_REQUIRE(blocks <= 0x7fffffffLL);
-        wush::fused_tq_smallm_kernel<<<(unsigned)blocks, 64, 0, stream>>>(x, t, q, s, rows, K);
+        const int64_t gx = (C + wush::kPairsPerWg - 1) / wush::kPairsPerWg;
+        WUSH_REQUIRE(gx <= 0x7fffffffLL && rows <= 65535);
+        wush::fused_tq_smallm_kernel<<<dim3((unsigned)gx, (unsigned)rows), 64, 0, stream>>>(x, t, q, s, rows, K);
     } else {
         const int64_t gx = (C + wush::kBlocksPerWg - 1) / wush::kBlocksPerWg;
         const int64_t gy = (rows + wush::kRowsPerWave - 1) / wush::kRowsPerWave;

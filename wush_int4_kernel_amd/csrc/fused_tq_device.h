@@ -50,15 +50,13 @@ __device__ __forceinline__ void load_bf16x32(const uint16_t* p, float (&v)[32]) 
     }
 }
 
-// Step 1: lane j stages x_j of pair p = r*C + c in LDS (xs_l, 32 floats) and
-// loads row j of T[c] as raw bf16 pairs (element 2d in the low half of word
-// d); returns x_j.  A barrier must follow before step 2.
+// Step 1: lane j stages x_j of pair (row r, block c) in LDS (xs_l, 32
+// floats) and loads row j of T[c] as raw bf16 pairs (element 2d in the low
+// half of word d); returns x_j.  A barrier must follow before step 2.
 __device__ __forceinline__ float tq_pair_load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ t,
-                                              int64_t K, int64_t p, bool active, int j, float* xs_l,
+                                              int64_t K, int64_t r, int64_t c, bool active, int j, float* xs_l,
                                               uint4 (&tj)[4]) {
-    const int64_t C = K >> 5;
-    const int64_t r = active ? p / C : 0;
-    const int64_t c = active ? p % C : 0;
+    if (!active) r = c = 0;
     const float xj = active ? bf16_to_f32(x[r * K + c * 32 + j]) : 0.0f;
     xs_l[j] = xj;
     const uint4* row = reinterpret_cast<const uint4*>(t + c * 1024 + j * 32);
