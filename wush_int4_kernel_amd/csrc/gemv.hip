@@ -393,7 +393,6 @@ __global__ __launch_bounds__(GL == 1 ? 1024 : 256) void gemv_ks_kernel(const uin
     for (int d = 0; d < kKsRing; ++d) load(d, d);
     __builtin_amdgcn_sched_barrier(0);
 
-
     // this lane's GL groups (64 * (GL * wave + t) + lane) of every activation
     // row; d' = kMagicBits + dot read as a float is kMagic + dot, so
     // fma(d', sx, -kMagic*sx) = dot*sx exactly
