@@ -86,9 +86,11 @@ int wush_fused_tq(const uint16_t *x, const uint16_t *t, uint8_t *q, uint16_t *s,
 int wush_gemv_int4(const uint8_t *xq, const uint16_t *xs, const uint8_t *wq, const uint16_t *ws,
                    uint16_t *y, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
-/* Bytes of workspace wush_gemm_s4 uses for (M, N, K); 0 when it needs none.
- * A caller may pass a larger buffer; a smaller one makes wush_gemm_s4 choose a
- * plan that needs no more than it is given. */
+/* Bytes of workspace wush_gemm_s4 uses for (M, N, K); 0 when it needs none:
+ * fp32 split-K partials, and for prefill shapes with N >= 8192 the
+ * activations converted once to fp16 operands (M*K*2 bytes, padded to 256
+ * rows).  A caller may pass a larger buffer; a smaller one makes wush_gemm_s4
+ * choose a plan that needs no more than it is given (same results). */
 size_t wush_gemm_s4_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* Group-scaled W4A4 GEMM, any M >= 1, K % 32 == 0: the product of
@@ -115,10 +117,11 @@ int wush_gemm_s4(const uint8_t *xq, const uint16_t *xs, const uint8_t *wq, const
 
 /* wush_gemm_s4 that allocates nothing and takes no workspace: its split-K
  * partials (if the plan splits K) go to the library's static scratch of
- * WUSH_GEMM_SCRATCH_BYTES on the current device.  Same plan, kernels and
- * results as wush_gemm_s4 given wush_gemm_s4_workspace_bytes(M, N, K) bytes of
- * workspace; a shape whose plan needs more scratch than that returns
- * WUSH_ERROR_SCRATCH_TOO_SMALL and launches nothing.  Nothing needs clearing
+ * WUSH_GEMM_SCRATCH_BYTES on the current device.  The same results as
+ * wush_gemm_s4, bit for bit, with the same split of K; prefill shapes convert
+ * their activations per tile instead of into the workspace.  A shape whose
+ * partials need more than the scratch returns WUSH_ERROR_SCRATCH_TOO_SMALL
+ * and launches nothing.  Nothing needs clearing
  * between calls: every partial is written before it is summed.  All calls on
  * one device share its scratch, so calls that overlap on one device (on
  * different streams, or from different host threads without ordering) race.

@@ -561,6 +561,38 @@ def test_gemm_h16_matches_oracle(capi, M, N, K):
         assert np.isfinite(y).all()
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 8192, 4096), (300, 33000, 512), (1030, 16400, 1024), (512, 8192, 1024)])
+def test_gemm_h16_preconverted_activations_bit_identical(capi, M, N, K):
+    # with a workspace of wush_gemm_s4_workspace_bytes, prefill plans with
+    # N >= 8192 convert the activations once into it (gemm_h16a); without
+    # that room they are converted per tile (gemm_h16w8): the same fp16
+    # operands in the same MFMA order, so the same bits.  (512, 8192, 1024)
+    # also splits K (2 slices), compared against the no-alloc entry point,
+    # whose scratch holds the partials but not the converted activations.
+    import torch
+    g = rng(4700 + M + N + K)
+    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    dx, dxs, dw, dws = _dev_operands(xq, xs, wq, ws)
+    wsb = capi.gemm_s4_workspace_bytes(M, N, K)
+    assert wsb >= 2 * M * K, "the plan should hold the converted activations"
+    work = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    y_a = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    capi.gemm_s4(dx.data_ptr(), dxs.data_ptr(), dw.data_ptr(), dws.data_ptr(), y_a.data_ptr(), M, N, K,
+                 work.data_ptr(), wsb, _stream())
+    y_t = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    if wsb > 4 * M * K:   # split-K partials too
+        capi.gemm_s4_noalloc(dx.data_ptr(), dxs.data_ptr(), dw.data_ptr(), dws.data_ptr(), y_t.data_ptr(),
+                             M, N, K, _stream())
+    else:
+        capi.gemm_s4(dx.data_ptr(), dxs.data_ptr(), dw.data_ptr(), dws.data_ptr(), y_t.data_ptr(), M, N, K,
+                     None, 0, _stream())
+    torch.cuda.synchronize()
+    assert torch.equal(y_a.view(torch.int16), y_t.view(torch.int16)), (M, N, K)
+    rows, cols = _sample(g, M, 24), _sample(g, N, 800)
+    ref = oracle.gemm_f64(xq[rows], xs[rows], wq[cols], ws[cols])
+    assert rel_fro(f16_tensor_f64(y_a)[np.ix_(rows, cols)], ref) < FRO_TOL
+
+
 def test_gemm_h16_int_exact_and_group_dots(capi):
     # unit scales and small codes: integer sums, exact in fp16; then scales 1
     # on one group only and 0 elsewhere: y = D[:, :, g] exactly

@@ -2,10 +2,12 @@
 (split-K partials in the library's static per-device scratch).
 
 It must give the same result as wush_gemm_s4 with a caller workspace of
-wush_gemm_s4_workspace_bytes(M, N, K) bytes -- the same plan and kernels, and
-every kernel is deterministic, so bit for bit -- on two calls in a row, the
-second with a smaller input (the scratch keeps the first call's contents), and
-reject a shape whose plan needs more than WUSH_GEMM_SCRATCH_BYTES.
+wush_gemm_s4_workspace_bytes(M, N, K) bytes -- the same split of K and the
+same kernels on these shapes (N < 8192: no activations converted into the
+workspace), every kernel deterministic, so bit for bit -- on two calls in a
+row, the second with a smaller input (the scratch keeps the first call's
+contents), and reject a shape whose partials need more than
+WUSH_GEMM_SCRATCH_BYTES.
 """
 from __future__ import annotations
 

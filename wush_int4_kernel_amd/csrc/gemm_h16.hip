@@ -375,6 +375,304 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
     }
 }
 
+// ------------------------------------------------ pre-converted activations
+// For wide weight matrices every 256-row activation tile above is converted
+// again by each of the N/256 column tiles.  gemm_h16a converts the
+// activations once (h16_prep_a_kernel, M x K x 2 bytes of workspace), in the
+// MFMA fragment layout, and streams them into a 4-slot LDS ring with
+// global_load_lds_dwordx4 (no VGPRs, issued 3 stages ahead by wavefronts
+// 0-3); wavefronts 4-7 convert the weight columns as above.  Same operands,
+// same MFMA order: bit-identical to gemm_h16w8_kernel.
+
+// a16 layout: [32-row block][group][K16 slice][64 lanes][16 B] (one block
+// and group: the two 1 KiB operand fragments of v_mfma_f32_32x32x16_f16);
+// ea[row] = the row's power-of-two shift.  Grid: (Mpad / 32, ceil(G / GB)).
+constexpr int kH16aPrepGroups = 32;
+constexpr int kH16aRing = 4;                      // LDS ring slots of the activation operand
+
+__global__ __launch_bounds__(256) void h16_prep_a_kernel(const uint8_t* __restrict__ xq,
+                                                         const uint16_t* __restrict__ xs,
+                                                         uint8_t* __restrict__ a16, int* __restrict__ ea,
+                                                         int M, int K) {
+    const int G = K >> 5;
+    const int rb = blockIdx.x;
+    const int tid = threadIdx.x;
+    __shared__ int se[32];
+    {
+        // largest |scale| of each of the block's 32 rows: 8 threads per row
+        const int r = tid >> 3, part = tid & 7;
+        const int row = rb * 32 + r;
+        uint32_t mx = 0;
+        if (row < M) {
+            const uint16_t* ps = xs + (size_t)row * G;
+            for (int g = part; g < G; g += 8) mx = max(mx, (uint32_t)(ps[g] & 0x7fffu));
+        }
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, 1));
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2));
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, 4));
+        if (part == 0) {
+            const int e = h16_shift(mx);
+            se[r] = e;
+            if (blockIdx.y == 0) ea[row] = e;     // rows past M: never stored
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < 32 * kH16aPrepGroups; i += 256) {
+        const int rr = i & 31, g = blockIdx.y * kH16aPrepGroups + (i >> 5);
+        if (g >= G) break;
+        const int row = rb * 32 + rr;
+        uint4 w = {0, 0, 0, 0};
+        float f = 0.0f;
+        if (row < M) {
+            w = *reinterpret_cast<const uint4*>(xq + (size_t)row * (K >> 1) + g * 16);
+            f = __uint_as_float((uint32_t)xs[(size_t)row * G + g] << 16);
+        }
+        h2 sc, sc16;
+        h16_scale(f, se[rr], sc, sc16);
+        uint8_t* dst = a16 + ((size_t)rb * G + g) * 2048 + rr * 16;
+        *reinterpret_cast<uint4*>(dst + 0) = h16_codes(w.x, sc, sc16);
+        *reinterpret_cast<uint4*>(dst + 512) = h16_codes(w.y, sc, sc16);
+        *reinterpret_cast<uint4*>(dst + 1024) = h16_codes(w.z, sc, sc16);
+        *reinterpret_cast<uint4*>(dst + 1536) = h16_codes(w.w, sc, sc16);
+    }
+}
+
+// s_waitcnt vmcnt(n) (n < 64) with the other counters left alone, and a
+// workgroup barrier after this wavefront's LDS writes (no wait on vector
+// memory: the activation DMA has its own explicit vmcnt waits)
+#define WUSH_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+#define WUSH_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
+typedef __attribute__((address_space(3))) void* h16_lds_ptr;
+typedef __attribute__((address_space(1))) void* h16_glb_ptr;
+// 16 bytes per lane from global memory straight into LDS at dst + 16 * lane
+// (dst wave-uniform)
+__device__ __forceinline__ void h16_dma16(const void* g, void* l) {
+    __builtin_amdgcn_global_load_lds((h16_glb_ptr)(g), (h16_lds_ptr)(l), 16, 0, 0);
+}
+
+// Tile order: workgroup id i runs on XCD i % 8; each XCD walks its column
+// tiles in groups of 8, row-major within a group, so the workgroups in
+// flight on an XCD share 8 weight column tiles and a few activation tiles
+// in its L2.
+__device__ __forceinline__ void h16a_tile(int& tm, int& tn) {
+    tm = blockIdx.y;
+    tn = blockIdx.x;
+    if ((gridDim.x & 7) != 0) return;
+    constexpr uint32_t kGroup = 8;
+    const uint32_t id = blockIdx.y * gridDim.x + blockIdx.x;
+    const uint32_t q = id >> 3, x = id & 7;
+    const uint32_t NR = gridDim.y, NC = gridDim.x >> 3;
+    const uint32_t gsize = kGroup * NR;
+    const uint32_t g = q / gsize, w = q % gsize;
+    const uint32_t width = min(kGroup, NC - g * kGroup);
+    tm = (int)(w / width);
+    tn = (int)((g * kGroup + w % width) * 8 + x);
+}
+
+// Scales 16-byte aligned and K % 256 == 0 (whole batches of 8 groups).
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_h16a_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ ea, const uint8_t* __restrict__ wq,
+                      const uint16_t* __restrict__ ws, uint16_t* __restrict__ y, float* __restrict__ partial, int M,
+                      int N, int K, int groups_per_split) {
+    // one LDS object per ring slot, so that the waitcnt insertion sees that an
+    // operand read of one slot does not alias a DMA into another
+    __shared__ __align__(16) uint8_t sA0[kH16Op], sA1[kH16Op], sA2[kH16Op], sA3[kH16Op];
+    __shared__ __align__(16) uint8_t sB0[kH16Op], sB1[kH16Op];
+    auto slotA = [&](int i) -> uint8_t* { return i == 0 ? sA0 : i == 1 ? sA1 : i == 2 ? sA2 : sA3; };
+    auto slotB = [&](int i) -> uint8_t* { return i == 0 ? sB0 : sB1; };
+    __shared__ int sh_e[512];                    // [0, 256) rows, [256, 512) columns
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    int tm, tn;
+    h16a_tile(tm, tn);
+    const int m0 = tm * kH16Tile;
+    const int n0 = tn * kH16Tile;
+    const int GR = K >> 5;
+    const int K2 = K >> 1;
+    const int gb = blockIdx.z * groups_per_split;
+    const int G = min(GR - gb, groups_per_split);
+
+    const bool wside = wave >= 4;
+    const int r = tid & 255;
+    const int limn = N - 1;
+    const uint16_t* ps = ws + (size_t)min(n0 + r, limn) * GR + gb;
+    int e = 0;
+    if (wside) {
+        uint32_t mx, mx2;
+        h16_row_max<true>(ps, ps, G, mx, mx2);
+        e = h16_shift(mx);
+        sh_e[tid] = e;
+    } else {
+        sh_e[tid] = ea[m0 + tid];                // ea covers the padded rows
+    }
+
+    // activation DMA of this wavefront (0-3): row blocks 2w, 2w + 1
+    const uint8_t* asrc = a16 + ((size_t)((m0 >> 5) + 2 * (wave & 3)) * GR + gb) * 2048 + lane * 16;
+    const size_t arb = (size_t)GR * 2048;        // next row block
+    auto issue_a = [&](int st, int slot) {
+        const int sc = min(st, G - 1);           // stages past the slice re-read the last one
+        uint8_t* dst = slotA(slot) + 2 * (wave & 3) * 1024;
+        const uint8_t* src = asrc + (size_t)sc * 2048;
+        h16_dma16(src, dst);
+        h16_dma16(src + 1024, dst + kH16Slice);
+        h16_dma16(src + arb, dst + 1024);
+        h16_dma16(src + arb + 1024, dst + kH16Slice + 1024);
+    };
+
+    // weight loads (wavefronts 4-7), as in gemm_h16w8_kernel
+    const int p4 = lane & 3;
+    const int wrow = n0 + (wave & 3) * 64 + (lane & ~3);
+    const uint8_t* qc[kH16Batch];
+#pragma unroll
+    for (int i = 0; i < kH16Batch; ++i) qc[i] = wq + (size_t)min(wrow + i, limn) * K2 + gb * 16 + p4 * 16;
+    struct Batch {
+        uint4 c[kH16Batch];
+        uint32_t s[kH16Batch];                   // s[0..1]: the 4 bf16 scales as two pairs
+    };
+    auto load_batch = [&](int b, Batch& rr) {
+        const int g0 = min(b * kH16Batch, G - kH16Batch) * 16;
+#pragma unroll
+        for (int i = 0; i < kH16Batch; ++i) rr.c[i] = *reinterpret_cast<const uint4*>(qc[i] + g0);
+        const uint2 v = *reinterpret_cast<const uint2*>(ps + min(b * kH16Batch, G - kH16Batch));
+        rr.s[0] = v.x; rr.s[1] = v.y;
+    };
+    const bool odd1 = (lane & 1) != 0;
+    const bool odd2 = (lane & 2) != 0;
+    auto transpose = [&](uint4 (&x)[kH16Batch]) {
+        uint4 z[kH16Batch];
+#pragma unroll
+        for (int i = 0; i < kH16Batch; ++i) {
+            const bool own = ((i & 1) != 0) == odd1;
+            const uint4 o = x[i ^ 1];
+            z[i].x = h16_xchg<0xB1>(x[i].x, o.x, !own);
+            z[i].y = h16_xchg<0xB1>(x[i].y, o.y, !own);
+            z[i].z = h16_xchg<0xB1>(x[i].z, o.z, !own);
+            z[i].w = h16_xchg<0xB1>(x[i].w, o.w, !own);
+        }
+#pragma unroll
+        for (int i = 0; i < kH16Batch; ++i) {
+            const bool own = ((i & 2) != 0) == odd2;
+            const uint4 o = z[i ^ 2];
+            x[i].x = h16_xchg<0x4E>(z[i].x, o.x, !own);
+            x[i].y = h16_xchg<0x4E>(z[i].y, o.y, !own);
+            x[i].z = h16_xchg<0x4E>(z[i].z, o.z, !own);
+            x[i].w = h16_xchg<0x4E>(z[i].w, o.w, !own);
+        }
+    };
+    const int wofs = (r >> 5) * 1024 + (r & 31) * 16;
+    auto convert = [&](int buf, Batch& rr, int i) {
+        if (i == 0) transpose(rr.c);
+        uint8_t* dst = slotB(buf) + wofs;
+        h2 sc, sc16;
+        h16_scale(h16_batch_scale<true>(rr.s, i), e, sc, sc16);
+        const uint32_t w4[4] = {rr.c[i].x, rr.c[i].y, rr.c[i].z, rr.c[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<uint4*>(dst + (j >> 1) * kH16Slice + (j & 1) * 512) = h16_codes(w4[j], sc, sc16);
+    };
+
+    v16f acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16f){0.0f};
+
+    const int rba = (wave >> 2) * 4;             // this wavefront's first 32-row block
+    const int rbb = (wave & 3) * 2;              // ... and first 32-column block
+    auto compute = [&](int abuf, int bbuf) {
+        const uint8_t* a0 = slotA(abuf);
+        const uint8_t* b0 = slotB(bbuf);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            h8 af[4], bf[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                af[i] = *reinterpret_cast<const h8*>(a0 + kk * kH16Slice + (rba + i) * 1024 + lane * 16);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                bf[j] = *reinterpret_cast<const h8*>(b0 + kk * kH16Slice + (rbb + j) * 1024 + lane * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // Both roles run the same number of barriers: one before the first stage
+    // and one after each of the G stages (G % 8 == 0).
+    if (wside) {
+        // weight wavefronts: convert the next stage's weights while multiplying
+        Batch R0, R1;
+        load_batch(0, R0);
+        load_batch(1, R1);
+        convert(0, R0, 0);
+        WUSH_LDS_BARRIER();
+        for (int s0 = 0; s0 < G; s0 += 2 * kH16Batch) {
+#pragma unroll
+            for (int j = 0; j < 2 * kH16Batch; ++j) {
+                compute(j & (kH16aRing - 1), j & 1);
+                if (j < kH16Batch - 1) convert((j + 1) & 1, R0, j + 1);
+                else if (j == kH16Batch - 1) convert(0, R1, 0);
+                else if (j < 2 * kH16Batch - 1) convert((j + 1) & 1, R1, j + 1 - kH16Batch);
+                else convert(0, R0, 0);
+                if (j == kH16Batch - 1) load_batch(s0 / kH16Batch + 2, R0);
+                if (j == 2 * kH16Batch - 1) load_batch(s0 / kH16Batch + 3, R1);
+                WUSH_LDS_BARRIER();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    } else {
+        // activation wavefronts: DMA the fragments kH16aRing - 1 stages ahead;
+        // 4 DMAs per stage, so vmcnt <= 8 means all but the last two stages landed
+        issue_a(0, 0);
+        issue_a(1, 1);
+        issue_a(2, 2);
+        WUSH_WAIT_VMCNT(8);
+        WUSH_LDS_BARRIER();
+        for (int s0 = 0; s0 < G; s0 += 2 * kH16Batch) {
+#pragma unroll
+            for (int j = 0; j < 2 * kH16Batch; ++j) {
+                issue_a(s0 + j + kH16aRing - 1, (j + kH16aRing - 1) & (kH16aRing - 1));
+                compute(j & (kH16aRing - 1), j & 1);
+                WUSH_WAIT_VMCNT(8);
+                WUSH_LDS_BARRIER();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        WUSH_WAIT_VMCNT(0);
+    }
+
+    const int half = lane >> 5;
+    const int l32 = lane & 31;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int cl = (rbb + j) * 32 + l32;
+        const int col = n0 + cl;
+        const int e_col = sh_e[256 + cl];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int rl = (rba + i) * 32 + 8 * (q >> 2) + 4 * half + (q & 3);
+                const int row = m0 + rl;
+                const int e_row = sh_e[rl];
+                float v = __builtin_ldexpf(acc[i][j][q], -(e_row + e_col));
+                if (e_row == kH16NonFinite || e_col == kH16NonFinite) v = __builtin_nanf("");
+                if (row < M && col < N) {
+                    if (partial != nullptr)
+                        partial[((size_t)blockIdx.z * M + row) * N + col] = v;
+                    else
+                        y[(size_t)row * N + col] = f32_to_f16_bits(v);
+                }
+            }
+        }
+    }
+}
+
 }  // namespace
 
 size_t gemm_h16_smem_bytes() { return 2 * kH16Buf + 2 * kH16Tile * sizeof(int); }
@@ -388,6 +686,31 @@ int gemm_h16_init_device() {
         e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_h16w8_kernel<false>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, smem);
     return (int)e;
+}
+
+size_t gemm_h16a_workspace_bytes(int64_t M, int64_t K) {
+    const int64_t mpad = (M + kH16Tile - 1) / kH16Tile * kH16Tile;
+    return (size_t)mpad * (size_t)K * 2 + (size_t)mpad * sizeof(int);
+}
+
+int launch_gemm_h16a(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
+                     uint16_t* y, float* partial, int M, int N, int K, int splits, int groups_per_split,
+                     void* a_ws, hipStream_t stream) {
+    const int G = K >> 5;
+    if (M <= 0 || N <= 0 || K <= 0 || K % 256 != 0 || splits < 1 || groups_per_split <= 0 ||
+        groups_per_split % 8 != 0 || (long long)splits * groups_per_split < G ||
+        (long long)(splits - 1) * groups_per_split >= G || (splits > 1 && partial == nullptr) || a_ws == nullptr ||
+        ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws) | reinterpret_cast<uintptr_t>(a_ws)) &
+         15u) != 0)
+        return (int)hipErrorInvalidValue;
+    const int mpad = (M + kH16Tile - 1) / kH16Tile * kH16Tile;
+    uint8_t* a16 = static_cast<uint8_t*>(a_ws);
+    int* ea = reinterpret_cast<int*>(a16 + (size_t)mpad * K * 2);
+    h16_prep_a_kernel<<<dim3((unsigned)(mpad / 32), (unsigned)((G + kH16aPrepGroups - 1) / kH16aPrepGroups)), 256, 0,
+                        stream>>>(xq, xs, a16, ea, M, K);
+    dim3 grid((unsigned)((N + kH16Tile - 1) / kH16Tile), (unsigned)(mpad / kH16Tile), (unsigned)splits);
+    gemm_h16a_kernel<<<grid, 512, 0, stream>>>(a16, ea, wq, ws, y, partial, M, N, K, groups_per_split);
+    return (int)hipGetLastError();
 }
 
 int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,

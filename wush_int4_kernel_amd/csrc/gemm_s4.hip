@@ -641,7 +641,20 @@ struct Plan {
     int splits;
     int groups_per_split;
     int tm, tn, sg;
+    bool a16 = false;  // cfg 5: activations pre-converted into the workspace (gemm_h16a)
 };
+
+// Workspace layout: fp32 split-K partials [splits][M][N] from offset 0, then
+// (a16 plans) the pre-converted activations at the next 256-byte boundary.
+static size_t plan_partial_bytes(const Plan& p, int64_t M, int64_t N) {
+    return p.splits > 1 ? (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+static size_t plan_a16_offset(const Plan& p, int64_t M, int64_t N) {
+    return (plan_partial_bytes(p, M, N) + 255) / 256 * 256;
+}
+static size_t plan_bytes(const Plan& p, int64_t M, int64_t N, int64_t K) {
+    return p.a16 ? plan_a16_offset(p, M, N) + gemm_h16a_workspace_bytes(M, K) : plan_partial_bytes(p, M, N);
+}
 
 #ifndef WUSH_PF_BM
 #define WUSH_PF_BM 2             // prefill tile: 32x32 blocks per wavefront along M
@@ -674,6 +687,12 @@ struct Plan {
 #endif
 #ifndef WUSH_H16_SPLIT_MIN_M
 #define WUSH_H16_SPLIT_MIN_M 512
+#endif
+// Pre-converted activations (gemm_h16a) when the weights have at least this
+// many columns, the scales are 16-byte aligned and the workspace has room
+// for M x K x 2 bytes more.
+#ifndef WUSH_H16A_MIN_N
+#define WUSH_H16A_MIN_N 8192
 #endif
 // 8 < M <= 32 streaming kernel (gemm_s4_stream32_kernel).  Measured on
 // MI355X against one wavefront per 32-row block: L70 (K=8192, N=57344)
@@ -731,7 +750,7 @@ constexpr int kStream32Waves = WUSH_S32_WAVES;
 // scales16: both scale tensors are 16-byte aligned (the streaming kernels
 // read them 8 groups at a time).
 static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available, bool allow_split,
-                      bool scales16) {
+                      bool scales16, bool allow_a16 = true) {
     Plan p;
     p.mr = 32;
     const int64_t G0 = K / 32;
@@ -771,6 +790,11 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
             p.cfg = 5; p.tm = 256; p.tn = 256; p.sg = 1;
             p.splits = s;
             p.groups_per_split = (int)(G0 / s);
+            if (allow_a16 && scales16 && N >= WUSH_H16A_MIN_N) {
+                Plan q = p;
+                q.a16 = true;
+                if (plan_bytes(q, M, N, K) <= ws_bytes_available) p.a16 = true;
+            }
             return p;
         }
     }
@@ -819,16 +843,22 @@ static void launch_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq
 template <bool PT>
 static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                     uint16_t* y, int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes,
-                    float alpha, const float* alpha_dev, hipStream_t stream) {
+                    float alpha, const float* alpha_dev, hipStream_t stream, bool allow_a16 = true) {
     const bool scales16 = ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws)) & 15u) == 0;
-    const Plan p = make_plan(M, N, K, workspace ? ws_bytes : 0, !PT, scales16);
+    // the pre-converted activations need a 16-byte aligned workspace
+    allow_a16 = allow_a16 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0;
+    const Plan p = make_plan(M, N, K, workspace ? ws_bytes : 0, !PT, scales16, allow_a16);
     WUSH_REQUIRE((N + p.tn - 1) / p.tn <= 0x7fffffffLL && (M + p.tm - 1) / p.tm <= 65535);
     float* partial = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int m = (int)M, n = (int)N, k = (int)K;
     if (p.cfg == 5) {
         if constexpr (!PT) {
-            const int st = launch_gemm_h16(xq, xs, wq, ws, y, partial, m, n, k, p.splits, p.groups_per_split,
-                                           stream);
+            const int st = p.a16 ? launch_gemm_h16a(xq, xs, wq, ws, y, partial, m, n, k, p.splits,
+                                                    p.groups_per_split,
+                                                    static_cast<uint8_t*>(workspace) + plan_a16_offset(p, M, N),
+                                                    stream)
+                                 : launch_gemm_h16(xq, xs, wq, ws, y, partial, m, n, k, p.splits,
+                                                   p.groups_per_split, stream);
             if (st != 0 || p.splits == 1) return st;
         }
     }
@@ -908,7 +938,7 @@ extern "C" {
 size_t wush_gemm_s4_workspace_bytes(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 32) return 0;
     const wush::Plan p = wush::make_plan(M, N, K, (size_t)-1, true, true);
-    return p.splits > 1 ? (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+    return wush::plan_bytes(p, M, N, K);
 }
 
 int wush_gemm_s4(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
@@ -933,16 +963,17 @@ int wush_gemm_s4_noalloc(const uint8_t* xq, const uint16_t* xs, const uint8_t* w
     WUSH_REQUIRE(xq && xs && wq && ws && y);
     WUSH_REQUIRE(((uintptr_t)xq & 15u) == 0 && ((uintptr_t)wq & 15u) == 0);
     WUSH_REQUIRE(((uintptr_t)xs & 1u) == 0 && ((uintptr_t)ws & 1u) == 0 && ((uintptr_t)y & 1u) == 0);
-    // the plan wush_gemm_s4 runs with wush_gemm_s4_workspace_bytes(M, N, K)
-    // bytes of workspace; its split-K partials go to this device's scratch
-    const size_t need = wush_gemm_s4_workspace_bytes(M, N, K);
+    // the plan wush_gemm_s4 runs with a workspace for its split-K partials
+    // only (no pre-converted activations, whose M*K*2 bytes would not fit);
+    // the partials go to this device's scratch
+    const size_t need = wush::plan_bytes(wush::make_plan(M, N, K, (size_t)-1, true, true, false), M, N, K);
     if (need > (size_t)WUSH_GEMM_SCRATCH_BYTES) return WUSH_ERROR_SCRATCH_TOO_SMALL;
     int dev = 0;
     const int st = wush::device_setup(&dev);
     if (st != 0) return st;
     void* scratch = need ? wush::scratch_address(dev) : nullptr;
     if (need && scratch == nullptr) return (int)hipErrorInvalidSymbol;
-    return wush::run_gemm<false>(xq, xs, wq, ws, y, M, N, K, scratch, need, 1.0f, nullptr, stream);
+    return wush::run_gemm<false>(xq, xs, wq, ws, y, M, N, K, scratch, need, 1.0f, nullptr, stream, false);
 }
 
 int wush_gemm_s4_tensor_scale(const uint8_t* xq, const uint8_t* wq, uint16_t* y, int64_t M, int64_t N,
