@@ -561,8 +561,10 @@ def test_gemm_h16_matches_oracle(capi, M, N, K):
         assert np.isfinite(y).all()
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 8192, 4096), (300, 33000, 512), (1030, 16400, 1024), (512, 8192, 1024)])
-def test_gemm_h16_preconverted_activations_bit_identical(capi, M, N, K):
+@pytest.mark.parametrize("M,N,K,wide", [(2048, 8192, 4096, False), (300, 33000, 512, False),
+                                         (1030, 16400, 1024, False), (512, 8192, 1024, False),
+                                         (512, 8192, 1024, True), (300, 33000, 512, True)])
+def test_gemm_h16_preconverted_activations_bit_identical(capi, M, N, K, wide):
     # with a workspace of wush_gemm_s4_workspace_bytes, prefill plans with
     # N >= 8192 convert the activations once into it (gemm_h16a); without
     # that room they are converted per tile (gemm_h16w8): the same fp16
@@ -570,8 +572,13 @@ def test_gemm_h16_preconverted_activations_bit_identical(capi, M, N, K):
     # also splits K (2 slices), compared against the no-alloc entry point,
     # whose scratch holds the partials but not the converted activations.
     import torch
-    g = rng(4700 + M + N + K)
-    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    # wide: activation scales spanning 2^35 within a row, so that tiny ones
+    # reach fp16's subnormal range and the per-slice shift matters
+    g = rng(4700 + M + N + K + wide)
+    if wide:
+        xq, xs, wq, ws = _random_code_operands(g, M, N, K, sx_exp=(100, 136), sw_exp=(118, 124))
+    else:
+        xq, xs, wq, ws = _rand_operands(g, M, N, K)
     dx, dxs, dw, dws = _dev_operands(xq, xs, wq, ws)
     wsb = capi.gemm_s4_workspace_bytes(M, N, K)
     assert wsb >= 2 * M * K, "the plan should hold the converted activations"

@@ -22,10 +22,10 @@ int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
                     hipStream_t stream);
 
 // The same product with the activations converted once into a workspace of
-// gemm_h16a_workspace_bytes(M, K) bytes (a_ws, 16-byte aligned) by a first
+// gemm_h16a_workspace_bytes(M, K, splits) bytes (a_ws, 16-byte aligned) by a first
 // kernel, then streamed into LDS; bit-identical to launch_gemm_h16.  Needs
 // 16-byte aligned scale tensors.
-size_t gemm_h16a_workspace_bytes(int64_t M, int64_t K);
+size_t gemm_h16a_workspace_bytes(int64_t M, int64_t K, int splits);
 int launch_gemm_h16a(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                      uint16_t* y, float* partial, int M, int N, int K, int splits, int groups_per_split,
                      void* a_ws, hipStream_t stream);

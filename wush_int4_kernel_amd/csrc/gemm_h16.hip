@@ -386,26 +386,34 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
 
 // a16 layout: [32-row block][group][K16 slice][64 lanes][16 B] (one block
 // and group: the two 1 KiB operand fragments of v_mfma_f32_32x32x16_f16);
-// ea[row] = the row's power-of-two shift.  Grid: (Mpad / 32, ceil(G / GB)).
-constexpr int kH16aPrepGroups = 32;
+// ea[slice][row] = the row's power-of-two shift over the K slice, as the
+// per-tile conversion computes it.  Grid: (Mpad / 32, G / 8): a workgroup
+// converts 32 rows x 8 groups, all in one slice (slices are whole multiples
+// of 8 groups).
+constexpr int kH16aPrepGroups = 8;
 constexpr int kH16aRing = 4;                      // LDS ring slots of the activation operand
 
 __global__ __launch_bounds__(256) void h16_prep_a_kernel(const uint8_t* __restrict__ xq,
                                                          const uint16_t* __restrict__ xs,
                                                          uint8_t* __restrict__ a16, int* __restrict__ ea,
-                                                         int M, int K) {
+                                                         int M, int K, int groups_per_split) {
     const int G = K >> 5;
+    const int mpad = gridDim.x * 32;
     const int rb = blockIdx.x;
+    const int g0 = blockIdx.y * kH16aPrepGroups;
+    const int slice = g0 / groups_per_split;
+    const int sg0 = slice * groups_per_split, sg1 = min(G, sg0 + groups_per_split);
     const int tid = threadIdx.x;
     __shared__ int se[32];
     {
-        // largest |scale| of each of the block's 32 rows: 8 threads per row
+        // largest |scale| of each of the block's 32 rows over the slice: 8
+        // threads per row
         const int r = tid >> 3, part = tid & 7;
         const int row = rb * 32 + r;
         uint32_t mx = 0;
         if (row < M) {
             const uint16_t* ps = xs + (size_t)row * G;
-            for (int g = part; g < G; g += 8) mx = max(mx, (uint32_t)(ps[g] & 0x7fffu));
+            for (int g = sg0 + part; g < sg1; g += 8) mx = max(mx, (uint32_t)(ps[g] & 0x7fffu));
         }
         mx = max(mx, (uint32_t)__shfl_xor((int)mx, 1));
         mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2));
@@ -413,28 +421,26 @@ __global__ __launch_bounds__(256) void h16_prep_a_kernel(const uint8_t* __restri
         if (part == 0) {
             const int e = h16_shift(mx);
             se[r] = e;
-            if (blockIdx.y == 0) ea[row] = e;     // rows past M: never stored
+            if (g0 == sg0) ea[(size_t)slice * mpad + row] = e;   // rows past M: never stored
         }
     }
     __syncthreads();
-    for (int i = tid; i < 32 * kH16aPrepGroups; i += 256) {
-        const int rr = i & 31, g = blockIdx.y * kH16aPrepGroups + (i >> 5);
-        if (g >= G) break;
-        const int row = rb * 32 + rr;
-        uint4 w = {0, 0, 0, 0};
-        float f = 0.0f;
-        if (row < M) {
-            w = *reinterpret_cast<const uint4*>(xq + (size_t)row * (K >> 1) + g * 16);
-            f = __uint_as_float((uint32_t)xs[(size_t)row * G + g] << 16);
-        }
-        h2 sc, sc16;
-        h16_scale(f, se[rr], sc, sc16);
-        uint8_t* dst = a16 + ((size_t)rb * G + g) * 2048 + rr * 16;
-        *reinterpret_cast<uint4*>(dst + 0) = h16_codes(w.x, sc, sc16);
-        *reinterpret_cast<uint4*>(dst + 512) = h16_codes(w.y, sc, sc16);
-        *reinterpret_cast<uint4*>(dst + 1024) = h16_codes(w.z, sc, sc16);
-        *reinterpret_cast<uint4*>(dst + 1536) = h16_codes(w.w, sc, sc16);
+    // thread: row rr, group g0 + tid / 32
+    const int rr = tid & 31, g = g0 + (tid >> 5);
+    const int row = rb * 32 + rr;
+    uint4 w = {0, 0, 0, 0};
+    float f = 0.0f;
+    if (row < M) {
+        w = *reinterpret_cast<const uint4*>(xq + (size_t)row * (K >> 1) + g * 16);
+        f = __uint_as_float((uint32_t)xs[(size_t)row * G + g] << 16);
     }
+    h2 sc, sc16;
+    h16_scale(f, se[rr], sc, sc16);
+    uint8_t* dst = a16 + ((size_t)rb * G + g) * 2048 + rr * 16;
+    *reinterpret_cast<uint4*>(dst + 0) = h16_codes(w.x, sc, sc16);
+    *reinterpret_cast<uint4*>(dst + 512) = h16_codes(w.y, sc, sc16);
+    *reinterpret_cast<uint4*>(dst + 1024) = h16_codes(w.z, sc, sc16);
+    *reinterpret_cast<uint4*>(dst + 1536) = h16_codes(w.w, sc, sc16);
 }
 
 // s_waitcnt vmcnt(n) (n < 64) with the other counters left alone, and a
@@ -506,7 +512,7 @@ void gemm_h16a_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
         e = h16_shift(mx);
         sh_e[tid] = e;
     } else {
-        sh_e[tid] = ea[m0 + tid];                // ea covers the padded rows
+        sh_e[tid] = ea[(size_t)blockIdx.z * (gridDim.y * kH16Tile) + m0 + tid];   // padded rows included
     }
 
     // activation DMA of this wavefront (0-3): row blocks 2w, 2w + 1
@@ -688,9 +694,9 @@ int gemm_h16_init_device() {
     return (int)e;
 }
 
-size_t gemm_h16a_workspace_bytes(int64_t M, int64_t K) {
+size_t gemm_h16a_workspace_bytes(int64_t M, int64_t K, int splits) {
     const int64_t mpad = (M + kH16Tile - 1) / kH16Tile * kH16Tile;
-    return (size_t)mpad * (size_t)K * 2 + (size_t)mpad * sizeof(int);
+    return (size_t)mpad * (size_t)K * 2 + (size_t)splits * (size_t)mpad * sizeof(int);
 }
 
 int launch_gemm_h16a(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
@@ -706,8 +712,8 @@ int launch_gemm_h16a(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, c
     const int mpad = (M + kH16Tile - 1) / kH16Tile * kH16Tile;
     uint8_t* a16 = static_cast<uint8_t*>(a_ws);
     int* ea = reinterpret_cast<int*>(a16 + (size_t)mpad * K * 2);
-    h16_prep_a_kernel<<<dim3((unsigned)(mpad / 32), (unsigned)((G + kH16aPrepGroups - 1) / kH16aPrepGroups)), 256, 0,
-                        stream>>>(xq, xs, a16, ea, M, K);
+    h16_prep_a_kernel<<<dim3((unsigned)(mpad / 32), (unsigned)(G / kH16aPrepGroups)), 256, 0, stream>>>(
+        xq, xs, a16, ea, M, K, groups_per_split);
     dim3 grid((unsigned)((N + kH16Tile - 1) / kH16Tile), (unsigned)(mpad / kH16Tile), (unsigned)splits);
     gemm_h16a_kernel<<<grid, 512, 0, stream>>>(a16, ea, wq, ws, y, partial, M, N, K, groups_per_split);
     return (int)hipGetLastError();

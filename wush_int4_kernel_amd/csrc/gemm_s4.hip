@@ -653,7 +653,7 @@ static size_t plan_a16_offset(const Plan& p, int64_t M, int64_t N) {
     return (plan_partial_bytes(p, M, N) + 255) / 256 * 256;
 }
 static size_t plan_bytes(const Plan& p, int64_t M, int64_t N, int64_t K) {
-    return p.a16 ? plan_a16_offset(p, M, N) + gemm_h16a_workspace_bytes(M, K) : plan_partial_bytes(p, M, N);
+    return p.a16 ? plan_a16_offset(p, M, N) + gemm_h16a_workspace_bytes(M, K, p.splits) : plan_partial_bytes(p, M, N);
 }
 
 #ifndef WUSH_PF_BM
