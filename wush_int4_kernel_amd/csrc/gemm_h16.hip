@@ -387,10 +387,8 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
 // a16 layout: [32-row block][group][K16 slice][64 lanes][16 B] (one block
 // and group: the two 1 KiB operand fragments of v_mfma_f32_32x32x16_f16);
 // ea[slice][row] = the row's power-of-two shift over the K slice, as the
-// per-tile conversion computes it.  Grid: (Mpad / 32, G / 8): a workgroup
-// converts 32 rows x 8 groups, all in one slice (slices are whole multiples
-// of 8 groups).
-constexpr int kH16aPrepGroups = 8;
+// per-tile conversion computes it.  Grid: (Mpad / 32, splits): a workgroup
+// converts 32 rows of one slice.
 constexpr int kH16aRing = 4;                      // LDS ring slots of the activation operand
 
 __global__ __launch_bounds__(256) void h16_prep_a_kernel(const uint8_t* __restrict__ xq,
@@ -400,47 +398,58 @@ __global__ __launch_bounds__(256) void h16_prep_a_kernel(const uint8_t* __restri
     const int G = K >> 5;
     const int mpad = gridDim.x * 32;
     const int rb = blockIdx.x;
-    const int g0 = blockIdx.y * kH16aPrepGroups;
-    const int slice = g0 / groups_per_split;
+    const int slice = blockIdx.y;
     const int sg0 = slice * groups_per_split, sg1 = min(G, sg0 + groups_per_split);
     const int tid = threadIdx.x;
     __shared__ int se[32];
     {
         // largest |scale| of each of the block's 32 rows over the slice: 8
-        // threads per row
+        // threads per row, 8 scales per load (slices are whole multiples of 8
+        // groups; scales 16-byte aligned)
         const int r = tid >> 3, part = tid & 7;
         const int row = rb * 32 + r;
-        uint32_t mx = 0;
+        u16x2 m2 = {0, 0};
         if (row < M) {
-            const uint16_t* ps = xs + (size_t)row * G;
-            for (int g = sg0 + part; g < sg1; g += 8) mx = max(mx, (uint32_t)(ps[g] & 0x7fffu));
+            const uint4* ps = reinterpret_cast<const uint4*>(xs + (size_t)row * G + sg0);
+            const int n8 = (sg1 - sg0) >> 3;
+#pragma unroll 4
+            for (int i = part; i < n8; i += 8) {
+                const uint4 v = ps[i];
+                m2 = __builtin_elementwise_max(m2, __builtin_elementwise_max(abs_bits2(v.x), abs_bits2(v.y)));
+                m2 = __builtin_elementwise_max(m2, __builtin_elementwise_max(abs_bits2(v.z), abs_bits2(v.w)));
+            }
         }
+        uint32_t mx = max((uint32_t)m2.x, (uint32_t)m2.y);
         mx = max(mx, (uint32_t)__shfl_xor((int)mx, 1));
         mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2));
         mx = max(mx, (uint32_t)__shfl_xor((int)mx, 4));
         if (part == 0) {
             const int e = h16_shift(mx);
             se[r] = e;
-            if (g0 == sg0) ea[(size_t)slice * mpad + row] = e;   // rows past M: never stored
+            ea[(size_t)slice * mpad + row] = e;   // rows past M: never stored
         }
     }
     __syncthreads();
-    // thread: row rr, group g0 + tid / 32
-    const int rr = tid & 31, g = g0 + (tid >> 5);
+    // thread: row tid % 32 of groups sg0 + tid / 32, + 8, ...
+    const int rr = tid & 31;
     const int row = rb * 32 + rr;
-    uint4 w = {0, 0, 0, 0};
-    float f = 0.0f;
-    if (row < M) {
-        w = *reinterpret_cast<const uint4*>(xq + (size_t)row * (K >> 1) + g * 16);
-        f = __uint_as_float((uint32_t)xs[(size_t)row * G + g] << 16);
+    const int e = se[rr];
+#pragma unroll 4
+    for (int g = sg0 + (tid >> 5); g < sg1; g += 8) {
+        uint4 w = {0, 0, 0, 0};
+        float f = 0.0f;
+        if (row < M) {
+            w = *reinterpret_cast<const uint4*>(xq + (size_t)row * (K >> 1) + g * 16);
+            f = __uint_as_float((uint32_t)xs[(size_t)row * G + g] << 16);
+        }
+        h2 sc, sc16;
+        h16_scale(f, e, sc, sc16);
+        uint8_t* dst = a16 + ((size_t)rb * G + g) * 2048 + rr * 16;
+        *reinterpret_cast<uint4*>(dst + 0) = h16_codes(w.x, sc, sc16);
+        *reinterpret_cast<uint4*>(dst + 512) = h16_codes(w.y, sc, sc16);
+        *reinterpret_cast<uint4*>(dst + 1024) = h16_codes(w.z, sc, sc16);
+        *reinterpret_cast<uint4*>(dst + 1536) = h16_codes(w.w, sc, sc16);
     }
-    h2 sc, sc16;
-    h16_scale(f, se[rr], sc, sc16);
-    uint8_t* dst = a16 + ((size_t)rb * G + g) * 2048 + rr * 16;
-    *reinterpret_cast<uint4*>(dst + 0) = h16_codes(w.x, sc, sc16);
-    *reinterpret_cast<uint4*>(dst + 512) = h16_codes(w.y, sc, sc16);
-    *reinterpret_cast<uint4*>(dst + 1024) = h16_codes(w.z, sc, sc16);
-    *reinterpret_cast<uint4*>(dst + 1536) = h16_codes(w.w, sc, sc16);
 }
 
 // s_waitcnt vmcnt(n) (n < 64) with the other counters left alone, and a
@@ -712,8 +721,8 @@ int launch_gemm_h16a(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, c
     const int mpad = (M + kH16Tile - 1) / kH16Tile * kH16Tile;
     uint8_t* a16 = static_cast<uint8_t*>(a_ws);
     int* ea = reinterpret_cast<int*>(a16 + (size_t)mpad * K * 2);
-    h16_prep_a_kernel<<<dim3((unsigned)(mpad / 32), (unsigned)(G / kH16aPrepGroups)), 256, 0, stream>>>(
-        xq, xs, a16, ea, M, K, groups_per_split);
+    h16_prep_a_kernel<<<dim3((unsigned)(mpad / 32), (unsigned)splits), 256, 0, stream>>>(xq, xs, a16, ea, M, K,
+                                                                                     groups_per_split);
     dim3 grid((unsigned)((N + kH16Tile - 1) / kH16Tile), (unsigned)(mpad / kH16Tile), (unsigned)splits);
     gemm_h16a_kernel<<<grid, 512, 0, stream>>>(a16, ea, wq, ws, y, partial, M, N, K, groups_per_split);
     return (int)hipGetLastError();

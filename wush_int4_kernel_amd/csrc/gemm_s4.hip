@@ -853,10 +853,9 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     const int m = (int)M, n = (int)N, k = (int)K;
     if (p.cfg == 5) {
         if constexpr (!PT) {
+            uint8_t* wsp = static_cast<uint8_t*>(workspace);
             const int st = p.a16 ? launch_gemm_h16a(xq, xs, wq, ws, y, partial, m, n, k, p.splits,
-                                                    p.groups_per_split,
-                                                    static_cast<uint8_t*>(workspace) + plan_a16_offset(p, M, N),
-                                                    stream)
+                                                    p.groups_per_split, wsp + plan_a16_offset(p, M, N), stream)
                                  : launch_gemm_h16(xq, xs, wq, ws, y, partial, m, n, k, p.splits,
                                                    p.groups_per_split, stream);
             if (st != 0 || p.splits == 1) return st;
