@@ -75,6 +75,17 @@ int wush_quant_int4(const void *x, int dtype, uint8_t *q, uint16_t *s,
 int wush_fused_tq(const uint16_t *x, const uint16_t *t, uint8_t *q, uint16_t *s,
                   int64_t rows, int64_t K, hipStream_t stream);
 
+/* The transform stage of wush_fused_tq's rows kernel alone, for one block:
+ * x'[r][j] = sum_i x[r][i] * t[j][i] (fp32, i ascending, every sum rounded),
+ * x rows*32 bf16, t 32*32 bf16, xp rows*32 fp32.  Runs the same code path as
+ * wush_fused_tq for the same values (fp32 MFMA steps, fma loop or mul-then-add
+ * loop, chosen per 64 rows).  No counterpart in the reference, whose transform
+ * is internal to fused_transform_quant_int4 (csrc/fused_tq_int4.cu:38-84): it
+ * lets tests compare x' itself, which the codes and scales see only near a
+ * rounding boundary. */
+int wush_fused_tq_transform32(const uint16_t *x, const uint16_t *t, float *xp, int64_t rows,
+                              hipStream_t stream);
+
 /* Decode GEMV for 1 <= M <= 8: y[m][n] = sum_g sx[m][g]*sw[n][g]*D[m][n][g]
  * with D the exact int32 dot of group g.  xq: M*K/2; xs: M*K/32; wq: N*K/2;
  * ws: N*K/32; y: M*N fp16.  The activations must fit 64 KiB of LDS

@@ -196,9 +196,9 @@ def test_fused_golden_fixture(capi):
 
 
 # The small-M kernel serves launches of at most 16384 (row, block) pairs; the
-# rows kernel the rest, in its DPP form below 1536 wavefronts (ceil(rows/64)
-# x K/32) and its SGPR form from there.  Shapes cover all three, with partial
-# 64-row sets and block counts that leave a workgroup's 4 blocks partial.
+# rows kernel the rest (fp32 MFMA steps when a wavefront's values are in
+# range).  Shapes cover both, with partial 64-row sets and block counts that
+# leave a workgroup's 4 blocks partial.
 @pytest.mark.parametrize("rows,K", [(1, 32), (1, 4096), (3, 96), (8, 8192), (63, 256), (64, 256),
                                     (65, 512), (130, 128), (383, 256), (384, 256), (385, 96),
                                     (256, 4096), (200, 4096), (1000, 1056),
@@ -215,29 +215,91 @@ def test_fused_random(capi, rows, K):
 
 @pytest.mark.parametrize("rows", [5, 2500, 12300])
 def test_fused_extreme_operands_both_loops(capi, rows):
-    # The rows kernel (here 2500 rows: DPP form, 12300 rows: SGPR form) and
-    # the small-M kernel (5 rows) run an fma loop when every nonzero |x| and
-    # |T| a wavefront multiplies lies in [2^-67, 2^51), and the mul-then-add
-    # loop otherwise.  Plant
-    # out-of-range values in some rows and T blocks (tiny, subnormal, huge,
-    # inf, NaN, at the range edges) so both loops and the vote between them
-    # run; every code and scale must still match the oracle bit for bit.
+    # The rows kernel (2500 and 12300 rows) runs fp32 MFMA steps when every
+    # nonzero |x| and |T| of a wavefront lies in [2^-56, 2^51), an fma loop
+    # when they lie in [2^-67, 2^51), and the mul-then-add loop otherwise;
+    # the small-M kernel (5 rows) the last two.  Plant out-of-range values in
+    # some rows and T blocks (tiny, subnormal, huge, inf, NaN, at the range
+    # edges) so every loop and the votes between them run; every code and
+    # scale must still match the oracle bit for bit.
     g = rng(2003 + rows)
     K = 256
     xb = outlier_activations(g, rows, K)
     tb = f32_to_bf16_bits(g.standard_normal((K // 32, 32, 32)) * 0.25)
     specials = [0x0001, 0x8001, 0x0080, 0x1DFF, 0x1E00, 0x58FF, 0x5900, 0x7F7F, 0x7F80, 0xFF80, 0x7FC0,
-                0x2000, 0x0C00, 0x6000]
+                0x2000, 0x0C00, 0x6000, 0x237F, 0xA37F, 0x2380]
     for r in range(0, rows, 7):
         xb[r, g.integers(0, K)] = specials[r % len(specials)]
     tb[1, 3, 5] = 0x0001            # subnormal T entry: block 1 takes mul + add
     tb[2, 0, 0] = 0x1DFF            # just below the range
     tb[3, 7, 9] = 0x58FF            # upper edge, still in range
     tb[4, 1, 1] = 0x5900            # just above the range
+    tb[5, 2, 30] = 0x237F           # below the MFMA range, inside the fma loop's
+    tb[6, 31, 0] = 0x2380           # lower edge of the MFMA range
     q, s = run_fused(capi, xb, tb)
     qo, so = oracle.fused_tq(xb, tb)
     assert np.array_equal(q, qo), np.argwhere(q != qo)[:5]
     assert np.array_equal(s, so), np.argwhere(s != so)[:5]
+
+
+def run_transform32(capi, xb: np.ndarray, tb: np.ndarray) -> np.ndarray:
+    import torch
+    rows = xb.shape[0]
+    xt, tt = to_dev_bf16(xb), to_dev_bf16(tb)
+    xp = torch.empty(rows * 32, dtype=torch.float32, device="cuda")
+    capi.fused_tq_transform32(xt.data_ptr(), tt.data_ptr(), xp.data_ptr(), rows, _stream())
+    torch.cuda.synchronize()
+    return xp.cpu().numpy().reshape(rows, 32)
+
+
+def _bf16_exp(g, shape, lo, hi, zeros=0.0):
+    """Random bf16 bit patterns: sign, exponent uniform in [lo, hi], 7-bit mantissa."""
+    e = g.integers(lo, hi + 1, size=shape) + 127
+    b = (g.integers(0, 2, size=shape) << 15) | (e << 7) | g.integers(0, 128, size=shape)
+    if zeros:
+        b = np.where(g.random(shape) < zeros, 0, b)
+    return b.astype(np.uint16)
+
+
+@pytest.mark.parametrize("family", ["normal", "wide", "ties", "fma_range", "specials"])
+def test_fused_transform_stage_bit_exact(capi, family):
+    # x' itself, from the rows kernel's transform stage, against the oracle's
+    # sequential fp32 sums: every value bit for bit (a NaN matches a NaN).
+    # "normal" and "wide" (exponents over the whole MFMA range [2^-56, 2^51),
+    # products from 2^-112 up, many roundings and absorptions) and "ties"
+    # (a leading product near 1.5, then products of exactly a half, a quarter
+    # or three quarters of its ulp: round-half-even decides most sums) run
+    # the MFMA steps; "fma_range" (values in [2^-67, 2^-56)) the fma loop;
+    # "specials" (subnormal, huge, inf, NaN in some rows) the mul-then-add
+    # loop next to MFMA wavefronts.
+    g = rng({"normal": 3101, "wide": 3102, "ties": 3103, "fma_range": 3104, "specials": 3105}[family])
+    rows = 64 * 7 + 19
+    if family == "normal":
+        xb = f32_to_bf16_bits(g.standard_normal((rows, 32)) * 3.0)
+        tb = f32_to_bf16_bits(g.standard_normal((1, 32, 32)) * 0.25)
+    elif family == "wide":
+        xb = _bf16_exp(g, (rows, 32), -56, 25, zeros=0.05)
+        tb = _bf16_exp(g, (1, 32, 32), -56, 25, zeros=0.05)
+    elif family == "ties":
+        xb = np.zeros((rows, 32), np.uint16)
+        xb[:, 0] = f32_to_bf16_bits(1.5 + g.integers(0, 4, rows) * 0.125)
+        xb[:, 1:] = f32_to_bf16_bits(np.ldexp(g.choice([-1.0, 1.0], (rows, 31)), -g.integers(22, 26, (rows, 31))))
+        tv = g.choice([1.0, 0.5, 0.75, -1.0, -0.5, 0.0], (1, 32, 32))
+        tv[:, :, 0] = 1.0
+        tb = f32_to_bf16_bits(tv)
+    elif family == "fma_range":
+        xb = _bf16_exp(g, (rows, 32), -60, 10)
+        xb[::3, 5] = 0x1E80                 # 2^-66: inside the fma loop's range only
+        tb = _bf16_exp(g, (1, 32, 32), -20, 5)
+    else:
+        xb = f32_to_bf16_bits(g.standard_normal((rows, 32)))
+        tb = f32_to_bf16_bits(g.standard_normal((1, 32, 32)) * 0.25)
+        for r, v in zip(range(3, rows, 37), [0x0001, 0x7F80, 0xFFC0, 0x7F7F, 0x8080, 0x5900]):
+            xb[r, (r * 7) % 32] = v
+    got = run_transform32(capi, xb, tb)
+    want = oracle.transform(xb, tb)
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert same.all(), (family, np.argwhere(~same)[:5], got[~same][:5], want[~same][:5])
 
 
 def test_fused_permutation_identity_zeros(capi):

@@ -21,6 +21,7 @@ SIGNATURES = {
     "wush_error_string": ([_I], ctypes.c_char_p),
     "wush_quant_int4": ([_P, _I, _P, _P, _I64, _P], _I),
     "wush_fused_tq": ([_P, _P, _P, _P, _I64, _I64, _P], _I),
+    "wush_fused_tq_transform32": ([_P, _P, _P, _I64, _P], _I),
     "wush_gemv_int4": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P], _I),
     "wush_gemm_s4_workspace_bytes": ([_I64, _I64, _I64], _SZ),
     "wush_gemm_s4": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P], _I),
@@ -87,6 +88,10 @@ ERROR_SCRATCH_TOO_SMALL = 0x57550001   # WUSH_ERROR_SCRATCH_TOO_SMALL
 
 def gemm_s4_noalloc(xq, xs, wq, ws, y, M, N, K, stream) -> None:
     _check(load().wush_gemm_s4_noalloc(xq, xs, wq, ws, y, M, N, K, stream), "wush_gemm_s4_noalloc")
+
+
+def fused_tq_transform32(x, t, xp, rows, stream) -> None:
+    _check(load().wush_fused_tq_transform32(x, t, xp, rows, stream), "wush_fused_tq_transform32")
 
 
 def mfma_selftest(a, b, c, stream) -> None:

@@ -5,22 +5,18 @@
 //   then the quant_int4 chain on the fp32 x' (no bf16 rounding of x').
 // Transformed activations never touch HBM.
 //
-// Three launch shapes, one numerics (the small-M per-pair steps live in
+// Two launch shapes, one numerics (the small-M per-pair steps live in
 // fused_tq_device.h):
 //  * rows kernel: lane = row, wavefront = 64 rows of one block c, 4
 //    wavefronts of a workgroup on 4 adjacent blocks of the same 64 rows (each
-//    row's 256 B of bf16 input is consumed by one workgroup).  T[c] is
-//    wave-uniform.  A product of two bf16 values is exact in fp32 unless an
-//    operand is extreme (tiny, huge, inf or NaN), and then fma(x, T, acc)
-//    equals the reference's acc + x*T bit for bit: when the wavefront's x and
-//    the block's T are all in range (checked per launch, almost always) the
-//    transform is 1024 fmas per lane instead of 1024 muls + 1024 adds.  T
-//    reaches the MACs in one of two ways:
-//     - SGPR form (launches of 1536 wavefronts or more): scalar loads into
-//       SGPRs, converted to fp32 on the SALU, every MAC takes an SGPR operand;
-//     - DPP form (fewer wavefronts, where the scalar loads' latency is not
-//       hidden): vector loads, 16 pairs per VGPR converted on the VALU, every
-//       MAC reads its T value from another lane through DPP row_newbcast.
+//    row's 256 B of bf16 input is consumed by one workgroup).  A product of
+//    two bf16 values is exact in fp32 unless an operand is extreme (tiny,
+//    huge, inf or NaN), and then fma(x, T, acc) equals the reference's
+//    acc + x*T bit for bit.  When the wavefront's x and T lie in the range
+//    that also keeps every partial sum normal (almost always), the transform
+//    runs as 32 rank-1 steps of the fp32 matrix cores (MFMA form below);
+//    otherwise as 1024 fmas per lane, or the mul-then-add sequence itself,
+//    with T in SGPRs (scalar loads converted on the SALU).
 //  * small-M kernel (at most 16384 (row, block) pairs: decode, small batches):
 //    32 lanes per (row, block), two adjacent blocks of one row per
 //    one-wavefront workgroup (grid: block pairs x rows) so a decode row
@@ -29,8 +25,6 @@
 //    wavefront's x and T are in range, as above); the group sums are then
 //    re-run in i-order by every lane from LDS (so they keep the sequential
 //    order) and lane pairs pack nibbles.
-#include <type_traits>
-
 #include "fused_tq_device.h"
 #include "../../include/wush_int4.h"
 
@@ -85,91 +79,87 @@ __device__ __forceinline__ void transform_block(const float (&xv)[32], const uin
     }
 }
 
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (N > 0) {
-        static_for<N - 1>(f);
-        f(std::integral_constant<int, N - 1>{});
-    }
-}
+// ------------------------------------------------------------- MFMA form
+// The transform as 32 rank-1 steps on the fp32 matrix cores.
+// v_mfma_f32_32x32x1_2b_f32 adds a[m] * b[n] to acc[m][n] for two
+// independent 32 x 32 blocks, one product per output and step, rounded once
+// to nearest even as fma rounds (x' itself is compared bit for bit with the
+// sequential sums, ties included, by test_fused_transform_stage_bit_exact
+// through wush_fused_tq_transform32).  With a[m] =
+// T[c][m][i] and b[n] = x[r0 + 32k + n][i] for block k, step i adds x_i *
+// T[c][j][i] to x'_j of the wavefront's 64 rows, i ascending: the
+// reference's sequence whenever every product is exact and nothing is
+// subnormal.  Both hold when every x and T value is zero or has magnitude in
+// [2^-56, 2^51): a product then has at most 16 significant bits, the lowest
+// at or above 2^-126, so every partial sum is a multiple of 2^-126 (zero or
+// normal) below 2^107.  Wavefronts with a value outside that range take the
+// fma or mul-then-add loop instead (transform_block).  The matrix cores run
+// the fp32 MACs at twice the VALU's rate; on gfx950 they do not overlap the
+// quantization's VALU work, so a wavefront costs 32 MFMAs of 64 cycles plus
+// about 600 VALU instructions (4096 rows, K = 8192: 43 -> 37 us).
+constexpr uint32_t kMfmaSafeLo = 0x2380u;        // bf16 magnitude bits of 2^-56
 
-// acc = acc + t' * x, where t' is t read from lane 16 * (lane / 16) + M
-// (DPP row_newbcast: lane M of each 16-lane row, broadcast to the row).
-// FAST: one v_fmac_f32_dpp, valid when t' * x is exact.  Otherwise
-// v_mul_f32_dpp then v_add_f32: the product and the sum rounded separately.
-template <int M, bool FAST>
-__device__ __forceinline__ void mac_bcast(float& acc, float t, float x) {
-    if constexpr (FAST) {
-        asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
-                     : "+v"(acc)
-                     : "v"(t), "v"(x), "n"(M));
-    } else {
-        float sum;
-        asm volatile("v_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf\n\t"
-                     "v_add_f32_e32 %0, %4, %0"
-                     : "=&v"(sum)
-                     : "v"(t), "v"(x), "n"(M), "v"(acc));
-        acc = sum;
-    }
-}
+typedef float v32f __attribute__((ext_vector_type(32)));
 
-// Four bf16 pairs -> their eight fp32 values (low halves, high halves).  The
-// trailing s_nop gives the two wait states a DPP read of a VGPR needs after a
-// VALU write of it.
-__device__ __forceinline__ void pairs_to_f32(const uint4& w, float (&lo)[4], float (&hi)[4]) {
-    asm volatile(
-        "v_lshlrev_b32_e32 %0, 16, %8\n\t"
-        "v_lshlrev_b32_e32 %1, 16, %9\n\t"
-        "v_lshlrev_b32_e32 %2, 16, %10\n\t"
-        "v_lshlrev_b32_e32 %3, 16, %11\n\t"
-        "v_and_b32_e32 %4, 0xffff0000, %8\n\t"
-        "v_and_b32_e32 %5, 0xffff0000, %9\n\t"
-        "v_and_b32_e32 %6, 0xffff0000, %10\n\t"
-        "v_and_b32_e32 %7, 0xffff0000, %11\n\t"
-        "s_nop 1"
-        : "=&v"(lo[0]), "=&v"(lo[1]), "=&v"(lo[2]), "=&v"(lo[3]),
-          "=&v"(hi[0]), "=&v"(hi[1]), "=&v"(hi[2]), "=&v"(hi[3])
-        : "v"(w.x), "v"(w.y), "v"(w.z), "v"(w.w));
-}
-
-// x'_j = sum_i x_i * T[c][j][i] for j = 0..31, i ascending, lane = row.
-// T[c] is read with vector loads in groups of 4 rows: lane m of every 16-lane
-// row loads row 4g + m/4, pairs 4(m%4)..4(m%4)+3 (16 bytes), so register k of
-// lane 4a + b holds pair 4b + k of row 4g + a, and row_newbcast:(4a + b)
-// hands that pair to every lane.  The 4 rows of a group are 4 interleaved
-// accumulation chains.  Loads run two groups ahead.
-template <bool FAST>
-__device__ __forceinline__ void transform_block_dpp(const float (&xv)[32], const uint4* __restrict__ tq4, int lane,
-                                                float (&xp)[32]) {
-    const uint4* src = tq4 + ((lane & 15) >> 2) * 4 + (lane & 3);
+// x'_j of the wavefront's 64 rows in xp (lane = row): the 32 MFMA steps, T
+// converted to fp32 as it is used, then the regrouping.  Block k's output is
+// in registers 16k .. 16k + 15: lane l, register e holds n = l % 32 and m =
+// 8 (e / 4) + 4 (l / 32) + e % 4.  Swapping block 1's registers of lanes 0-31
+// with block 0's of lanes 32-63 leaves lane l with all 32 x'_j of row r0 + l:
+// j = 8a + b from the first register of the pair, 8a + 4 + b from the second
+// (e = 4a + b).
+__device__ __forceinline__ void tq_mfma_steps(const uint32_t (&ut)[16], const float (&xv)[32], float (&xp)[32]) {
+    v32f acc = (v32f){0.0f};
 #pragma unroll
-    for (int j = 0; j < 32; ++j) xp[j] = 0.0f;
-    uint4 raw_next = src[16];
-    float lo[2][4], hi[2][4];
-    pairs_to_f32(src[0], lo[0], hi[0]);
-    static_for<8>([&](auto gc) {
-        constexpr int g = decltype(gc)::value;
-        uint4 raw_after;
-        if constexpr (g + 2 < 8) raw_after = src[(g + 2) * 16];
-        if constexpr (g + 1 < 8) pairs_to_f32(raw_next, lo[(g + 1) & 1], hi[(g + 1) & 1]);
-        static_for<16>([&](auto pc) {
-            constexpr int p = decltype(pc)::value, b = p / 4, k = p % 4;
-            static_for<4>([&](auto ac) {
-                constexpr int a = decltype(ac)::value;
-                mac_bcast<4 * a + b, FAST>(xp[4 * g + a], lo[g & 1][k], xv[2 * p]);
-            });
-            static_for<4>([&](auto ac) {
-                constexpr int a = decltype(ac)::value;
-                mac_bcast<4 * a + b, FAST>(xp[4 * g + a], hi[g & 1][k], xv[2 * p + 1]);
-            });
-        });
-        if constexpr (g + 2 < 8) raw_next = raw_after;
-    });
+    for (int d = 0; d < 16; ++d) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x1f32(bf16_to_f32(ut[d] & 0xffffu), xv[2 * d], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x1f32(__uint_as_float(ut[d] & 0xffff0000u), xv[2 * d + 1], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[e]), __float_as_uint(acc[16 + e]),
+                                                         false, false);
+        xp[8 * (e >> 2) + (e & 3)] = __uint_as_float(pr[0]);
+        xp[8 * (e >> 2) + 4 + (e & 3)] = __uint_as_float(pr[1]);
+    }
 }
 
-// One wavefront: 64 rows (r0 + lane) of block c; 4 wavefronts of a workgroup
-// take 4 adjacent blocks.  DPP picks transform_block_dpp, else the SGPR form.
-template <bool DPP>
+// The rows kernel's transform stage: x'_j (j = 0..31) of block c for the row
+// at xrow (row stride K), lane = row.  x and T are read as bf16 pairs; the
+// wavefront's range vote picks the MFMA steps, the fma loop or the
+// mul-then-add loop (T through SGPRs for the last two).
+__device__ __forceinline__ void tq_rows_transform(const uint16_t* __restrict__ xrow, const uint16_t* __restrict__ t,
+                                                  int64_t c, int lane, float (&xp)[32]) {
+    // lane l: row l % 32 of T[c] (the MFMA's A operand, both blocks) and x of
+    // its own row (the B operand)
+    const uint32_t* tc = reinterpret_cast<const uint32_t*>(t + c * 1024);
+    const uint4* t4 = reinterpret_cast<const uint4*>(tc + (lane & 31) * 16);
+    const uint4* p4 = reinterpret_cast<const uint4*>(xrow + c * 32);
+    uint32_t ut[16], ux[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint4 a = t4[k], b = p4[k];
+        ut[4 * k] = a.x; ut[4 * k + 1] = a.y; ut[4 * k + 2] = a.z; ut[4 * k + 3] = a.w;
+        ux[4 * k] = b.x; ux[4 * k + 1] = b.y; ux[4 * k + 2] = b.z; ux[4 * k + 3] = b.w;
+    }
+    // range of the wavefront's x and T (each lane checks its T row)
+    BfRange rg;
+    float xv[32];
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+        xv[2 * d] = bf16_to_f32(ux[d] & 0xffffu);
+        xv[2 * d + 1] = __uint_as_float(ux[d] & 0xffff0000u);
+        rg.add(ux[d]);
+        rg.add(ut[d]);
+    }
+    if (__all(rg.safe_from(kMfmaSafeLo))) tq_mfma_steps(ut, xv, xp);
+    else if (__all(rg.safe())) transform_block<true>(xv, tc, xp);
+    else transform_block<false>(xv, tc, xp);
+}
+
+// One wavefront: 64 rows (r0 + lane) of block c; the 4 wavefronts of a
+// workgroup take 4 adjacent blocks.  Lanes past the last row read row r0
+// (their results are not stored).
 __global__ __launch_bounds__(256) void fused_tq_rows_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ t,
                                                             uint8_t* __restrict__ q,
@@ -184,50 +174,30 @@ __global__ __launch_bounds__(256) void fused_tq_rows_kernel(const uint16_t* __re
     const int64_t r = r0 + lane;
     const bool active = r < rows;
 
-    // T[c][j][i] as bf16 pairs (i even in the low half), wave-uniform.  Each
-    // lane range-checks 16 of the block's 1024 entries; these loads go first
-    // so that the check waits for them alone.
-    const uint32_t* tc = reinterpret_cast<const uint32_t*>(t + c * 1024);
-    const uint4* t4 = reinterpret_cast<const uint4*>(tc) + lane * 2;
-    const uint4 ta = t4[0], tb = t4[1];
-    // Lanes past the last row read row r0 (their results are not stored).
-    const uint4* p4 = reinterpret_cast<const uint4*>(x + (active ? r : r0) * K + c * 32);
-    uint4 raw[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) raw[k] = p4[k];
-    BfRange tr;
-    tr.add(ta.x); tr.add(ta.y); tr.add(ta.z); tr.add(ta.w);
-    tr.add(tb.x); tr.add(tb.y); tr.add(tb.z); tr.add(tb.w);
-
-    float xv[32];
-    BfRange xr;
-    const uint32_t* u = &raw[0].x;
-#pragma unroll
-    for (int d = 0; d < 16; ++d) {
-        xv[2 * d] = bf16_to_f32(u[d] & 0xffffu);
-        xv[2 * d + 1] = __uint_as_float(u[d] & 0xffff0000u);
-        xr.add(u[d]);
-    }
-    // x_i * T[c][j][i] of two bf16 values is exact in fp32 when both lie in
-    // the safe range, and then fma(x, T, acc) == acc + x*T bit for bit: one
-    // fma per MAC instead of a mul and an add.  Otherwise the sequential
-    // mul-then-add form, which also carries inf / NaN / underflow exactly.
     float xp[32];
-    const bool fast = __all(xr.safe() & tr.safe());
-    if constexpr (DPP) {
-        const uint4* tq4 = reinterpret_cast<const uint4*>(tc);
-        if (fast) transform_block_dpp<true>(xv, tq4, lane, xp);
-        else transform_block_dpp<false>(xv, tq4, lane, xp);
-    } else {
-        if (fast) transform_block<true>(xv, tc, xp);
-        else transform_block<false>(xv, tc, xp);
-    }
-
+    tq_rows_transform(x + (active ? r : r0) * K, t, c, lane, xp);
     uint32_t w[4];
     const uint32_t sb = quant_group32(xp, w);
     if (active) {
         reinterpret_cast<uint4*>(q + (r * C + c) * 16)[0] = make_uint4(w[0], w[1], w[2], w[3]);
         s[r * C + c] = (uint16_t)sb;
+    }
+}
+
+// The transform stage alone, for one block: x rows x 32, xp rows x 32 fp32.
+__global__ __launch_bounds__(64) void fused_tq_transform32_kernel(const uint16_t* __restrict__ x,
+                                                                  const uint16_t* __restrict__ t,
+                                                                  float* __restrict__ xp, int64_t rows) {
+    const int lane = threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.x * kRowsPerWave;
+    const int64_t r = r0 + lane;
+    const bool active = r < rows;
+    float v[32];
+    tq_rows_transform(x + (active ? r : r0) * 32, t, 0, lane, v);
+    if (active) {
+#pragma unroll
+        for (int j = 0; j < 32; j += 4)
+            *reinterpret_cast<float4*>(xp + r * 32 + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
     }
 }
 
@@ -268,13 +238,6 @@ __global__ __launch_bounds__(64) void fused_tq_smallm_kernel(const uint16_t* __r
 #ifndef WUSH_TQ_SMALLM_PAIRS
 #define WUSH_TQ_SMALLM_PAIRS 16384
 #endif
-// Rows-kernel launches with fewer wavefronts than this take the DPP form
-// (K=4096: 512 rows 6.4 vs 8.5 us; 768 rows 9.2 vs 9.1 us; 2048 rows 16.2 vs
-// 14.2 us for DPP vs SGPR).
-#ifndef WUSH_TQ_DPP_WAVES
-#define WUSH_TQ_DPP_WAVES 1536
-#endif
-
 extern "C" int wush_fused_tq(const uint16_t* x, const uint16_t* t, uint8_t* q, uint16_t* s,
                              int64_t rows, int64_t K, hipStream_t stream) {
     WUSH_REQUIRE(rows >= 0 && K > 0 && K % 32 == 0);
@@ -292,10 +255,19 @@ extern "C" int wush_fused_tq(const uint16_t* x, const uint16_t* t, uint8_t* q, u
         const int64_t gy = (rows + wush::kRowsPerWave - 1) / wush::kRowsPerWave;
         WUSH_REQUIRE(gx <= 0x7fffffffLL && gy <= 65535);
         const dim3 grid((unsigned)gx, (unsigned)gy);
-        if (gy * C < WUSH_TQ_DPP_WAVES)
-            wush::fused_tq_rows_kernel<true><<<grid, 256, 0, stream>>>(x, t, q, s, rows, K);
-        else
-            wush::fused_tq_rows_kernel<false><<<grid, 256, 0, stream>>>(x, t, q, s, rows, K);
+        wush::fused_tq_rows_kernel<<<grid, 256, 0, stream>>>(x, t, q, s, rows, K);
     }
+    return (int)hipGetLastError();
+}
+
+extern "C" int wush_fused_tq_transform32(const uint16_t* x, const uint16_t* t, float* xp, int64_t rows,
+                                         hipStream_t stream) {
+    WUSH_REQUIRE(rows >= 0);
+    if (rows == 0) return (int)hipSuccess;
+    WUSH_REQUIRE(x && t && xp);
+    WUSH_REQUIRE(((uintptr_t)x & 15u) == 0 && ((uintptr_t)t & 15u) == 0 && ((uintptr_t)xp & 15u) == 0);
+    const int64_t g = (rows + wush::kRowsPerWave - 1) / wush::kRowsPerWave;
+    WUSH_REQUIRE(g <= 0x7fffffffLL);
+    wush::fused_tq_transform32_kernel<<<(unsigned)g, 64, 0, stream>>>(x, t, xp, rows);
     return (int)hipGetLastError();
 }

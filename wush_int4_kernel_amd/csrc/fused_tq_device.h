@@ -30,11 +30,14 @@ struct BfRange {
         mx = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, mx), m));
         mn = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, mn), m1));
     }
-    __device__ __forceinline__ bool safe() const {
+    // every nonzero magnitude at least the bf16 magnitude bits lo (and below
+    // 2^51)
+    __device__ __forceinline__ bool safe_from(uint32_t lo) const {
         const uint32_t mx_lo = mx & 0xffffu, mx_hi = mx >> 16;
         const uint32_t mn_lo = mn & 0xffffu, mn_hi = mn >> 16;
-        return (mx_lo <= 0x58ffu) & (mx_hi <= 0x58ffu) & (mn_lo >= 0x1dffu) & (mn_hi >= 0x1dffu);
+        return (mx_lo <= 0x58ffu) & (mx_hi <= 0x58ffu) & (mn_lo >= lo - 1) & (mn_hi >= lo - 1);
     }
+    __device__ __forceinline__ bool safe() const { return safe_from(0x1e00u); }
 };
 
 __device__ __forceinline__ void load_bf16x32(const uint16_t* p, float (&v)[32]) {
