@@ -124,23 +124,20 @@ __device__ __forceinline__ void tq_mfma_steps(const uint32_t (&ut)[16], const fl
     }
 }
 
-// The rows kernel's transform stage: x'_j (j = 0..31) of block c for the row
-// at xrow (row stride K), lane = row.  x and T are read as bf16 pairs; the
-// wavefront's range vote picks the MFMA steps, the fma loop or the
-// mul-then-add loop (T through SGPRs for the last two).
-__device__ __forceinline__ void tq_rows_transform(const uint16_t* __restrict__ xrow, const uint16_t* __restrict__ t,
+// The rows kernel's transform stage: x'_j (j = 0..31) of block c from the
+// lane's 32 x values (ux: 16 bf16 pairs), lane = row.  The wavefront's range
+// vote picks the MFMA steps, the fma loop or the mul-then-add loop (T
+// through SGPRs for the last two).
+__device__ __forceinline__ void tq_rows_transform(const uint32_t (&ux)[16], const uint16_t* __restrict__ t,
                                                   int64_t c, int lane, float (&xp)[32]) {
-    // lane l: row l % 32 of T[c] (the MFMA's A operand, both blocks) and x of
-    // its own row (the B operand)
+    // lane l: row l % 32 of T[c], the MFMA's A operand for both blocks
     const uint32_t* tc = reinterpret_cast<const uint32_t*>(t + c * 1024);
     const uint4* t4 = reinterpret_cast<const uint4*>(tc + (lane & 31) * 16);
-    const uint4* p4 = reinterpret_cast<const uint4*>(xrow + c * 32);
-    uint32_t ut[16], ux[16];
+    uint32_t ut[16];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint4 a = t4[k], b = p4[k];
+        const uint4 a = t4[k];
         ut[4 * k] = a.x; ut[4 * k + 1] = a.y; ut[4 * k + 2] = a.z; ut[4 * k + 3] = a.w;
-        ux[4 * k] = b.x; ux[4 * k + 1] = b.y; ux[4 * k + 2] = b.z; ux[4 * k + 3] = b.w;
     }
     // range of the wavefront's x and T (each lane checks its T row)
     BfRange rg;
@@ -157,30 +154,73 @@ __device__ __forceinline__ void tq_rows_transform(const uint16_t* __restrict__ x
     else transform_block<false>(xv, tc, xp);
 }
 
-// One wavefront: 64 rows (r0 + lane) of block c; the 4 wavefronts of a
-// workgroup take 4 adjacent blocks.  Lanes past the last row read row r0
-// (their results are not stored).
+__device__ __forceinline__ void load_words16(const uint16_t* __restrict__ p, uint32_t (&u)[16]) {
+    const uint4* p4 = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint4 v = p4[k];
+        u[4 * k] = v.x; u[4 * k + 1] = v.y; u[4 * k + 2] = v.z; u[4 * k + 3] = v.w;
+    }
+}
+
+// Workgroup: 64 rows (r0 ..) x 4 adjacent blocks (cb ..); wavefront w
+// computes block cb + w, lane = row.  Each row's 256 input bytes and its 64
+// bytes of codes and 8 of scales are contiguous, but a lane-per-row access
+// touches one row per lane.  So the workgroup stages both through LDS: 16
+// lanes read one row's 256 bytes (4 rows per load instruction), and 4 lanes
+// write one row's codes and scales.  Rows past the last row and blocks past
+// the last block are read clamped and not stored.
+constexpr int kTqXPitch = 272;                   // LDS bytes per staged input row (256 + 16: no bank conflicts)
+constexpr int kTqQPitch = 80;                    // ... per staged code row (64 + 16)
+
 __global__ __launch_bounds__(256) void fused_tq_rows_kernel(const uint16_t* __restrict__ x,
                                                             const uint16_t* __restrict__ t,
                                                             uint8_t* __restrict__ q,
                                                             uint16_t* __restrict__ s,
                                                             int64_t rows, int64_t K) {
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int lane = threadIdx.x & 63;
+    __shared__ __align__(16) uint8_t sx[kRowsPerWave * kTqXPitch];
+    __shared__ __align__(16) uint8_t sq[kRowsPerWave * kTqQPitch];
+    __shared__ __align__(16) uint16_t ss[kRowsPerWave * kBlocksPerWg];
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
     const int64_t C = K >> 5;
-    const int64_t c = (int64_t)blockIdx.x * kBlocksPerWg + wave;
-    if (c >= C) return;
+    const int64_t cb = (int64_t)blockIdx.x * kBlocksPerWg;
     const int64_t r0 = (int64_t)blockIdx.y * kRowsPerWave;
-    const int64_t r = r0 + lane;
-    const bool active = r < rows;
 
+    // coalesced input: wavefront w loads rows 16w .. 16w + 15 of the tile
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int rl = 16 * wave + 4 * k + (lane >> 4);
+        const int64_t rr = min(r0 + rl, rows - 1);
+        const int64_t cc = min(cb + ((lane & 15) >> 2), C - 1);
+        const uint4 v = *reinterpret_cast<const uint4*>(x + rr * K + cc * 32 + (lane & 3) * 8);
+        *reinterpret_cast<uint4*>(sx + rl * kTqXPitch + (lane & 15) * 16) = v;
+    }
+    __syncthreads();
+    uint32_t ux[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint4 v = *reinterpret_cast<const uint4*>(sx + lane * kTqXPitch + wave * 64 + k * 16);
+        ux[4 * k] = v.x; ux[4 * k + 1] = v.y; ux[4 * k + 2] = v.z; ux[4 * k + 3] = v.w;
+    }
+
+    const int64_t c = min(cb + wave, C - 1);
     float xp[32];
-    tq_rows_transform(x + (active ? r : r0) * K, t, c, lane, xp);
+    tq_rows_transform(ux, t, c, lane, xp);
     uint32_t w[4];
     const uint32_t sb = quant_group32(xp, w);
-    if (active) {
-        reinterpret_cast<uint4*>(q + (r * C + c) * 16)[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        s[r * C + c] = (uint16_t)sb;
+    *reinterpret_cast<uint4*>(sq + lane * kTqQPitch + wave * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    ss[lane * kBlocksPerWg + wave] = (uint16_t)sb;
+    __syncthreads();
+
+    // coalesced output: wavefront w stores rows 16w .. 16w + 15, 4 lanes a row
+    const int rl = 16 * wave + (lane >> 2);
+    const int bl = lane & 3;
+    const int64_t r = r0 + rl, cs = cb + bl;
+    if (r < rows && cs < C) {
+        *reinterpret_cast<uint4*>(q + (r * C + cs) * 16) = *reinterpret_cast<const uint4*>(sq + rl * kTqQPitch + bl * 16);
+        s[r * C + cs] = ss[rl * kBlocksPerWg + bl];
     }
 }
 
@@ -192,8 +232,10 @@ __global__ __launch_bounds__(64) void fused_tq_transform32_kernel(const uint16_t
     const int64_t r0 = (int64_t)blockIdx.x * kRowsPerWave;
     const int64_t r = r0 + lane;
     const bool active = r < rows;
+    uint32_t ux[16];
+    load_words16(x + (active ? r : r0) * 32, ux);
     float v[32];
-    tq_rows_transform(x + (active ? r : r0) * 32, t, 0, lane, v);
+    tq_rows_transform(ux, t, 0, lane, v);
     if (active) {
 #pragma unroll
         for (int j = 0; j < 32; j += 4)
