@@ -54,7 +54,6 @@ METRIC = "µs/layer + speedup vs hipBLASLt bf16, K=8192 N=57344 at M=1/8/32/4096
 K_L70, N_L70 = 8192, 57344
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
-VALU_PEAK_LANE_OPS = 256 * 4 * 16 * 2.4e9   # 256 CUs x 4 SIMDs x 16 lanes per cycle x 2.4 GHz (no packed fp32)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_int4_l70_m1_traffic.txt")
 
 
@@ -84,6 +83,7 @@ def parse():
 
 
 FP16_PEAK_TFLOPS = 2500.0       # dense fp16 MFMA (the prefill kernel's instruction)
+F32_MFMA_PEAK_TFLOPS = 157.3    # fp32 MFMA (the fused transform's instruction)
 
 
 def capture(fns):
@@ -490,12 +490,12 @@ def main():
     Tc2 = compute_wush_transform(acts_c(512).double(), Wc2.double()).to(torch.bfloat16).contiguous()
     t = time_med5(capture([lambda: _C.fused_transform_quant_int4(Xc2, Tc2)] * 10), 10, 4)
     tq_bytes = 2 * Mc * Kc + 64 * Kc + Mc * Kc // 2 + Mc * Kc // 16
-    tq_lane_ops = 32 * Mc * Kc          # one exact-product fma per MAC, 32 MACs per element
+    tq_macs = 32 * Mc * Kc              # 32 MACs per element, on the fp32 matrix cores
     ops["fused_tq_cfg2"] = {
         "us": round(t * 1e6, 2), "shape": f"X {Mc}x{Kc} bf16, T {Kc // 32}x32x32",
         "hbm_bytes": tq_bytes, "hbm_gbs": round(tq_bytes / t / 1e9, 1),
         "hbm_frac": round(tq_bytes / t / 1e9 / HBM_PEAK_GBS, 4),
-        "valu_lane_ops": tq_lane_ops, "valu_frac": round(tq_lane_ops / t / VALU_PEAK_LANE_OPS, 4),
+        "fp32_macs": tq_macs, "mfma_f32_frac": round(2 * tq_macs / t / (F32_MFMA_PEAK_TFLOPS * 1e12), 4),
     }
     # a2/a3: quant_int4 of one Llama-70B weight tensor (N x K bf16), HBM-bound
     t = time_med5(capture([lambda: _C.quant_int4(Wt)] * 2), 2, 2)
