@@ -252,12 +252,20 @@ def sweep(args):
         tb = time_med5(capture([lambda: torch.matmul(X, blas_w[0].t())]), 1, reps)
         X16 = X.half()
         th = time_med5(capture([lambda: torch.matmul(X16, half_w[0].t())]), 1, reps)
+        # the same with graph_steps calls per replay, over the weight copies
+        gs = args.graph_steps
+        r12 = max(1, reps // gs)
+        t4g = time_med5(graph_of(lambda i: (lambda c=copies[i % len(copies)]: _C.w4a4_gemm_s4(xq, xs, c[0], c[1])),
+                                 gs), gs, r12)
+        tbg = time_med5(graph_of(lambda i: (lambda Wc=blas_w[i % len(blas_w)]: torch.matmul(X, Wc.t())), gs), gs, r12)
         gemm_rows.append({"M": M, "N": N, "K": K, "w4a4_gemm_s4_us": round(t4 * 1e6, 2),
                           "tflops": round(2 * M * N * K / t4 / 1e12, 2), "hipblaslt_fp16_us": round(th * 1e6, 2),
                           "hipblaslt_bf16_us": round(tb * 1e6, 2), "speedup_vs_fp16": round(th / t4, 3),
-                          "speedup_vs_bf16": round(tb / t4, 3)})
+                          "speedup_vs_bf16": round(tb / t4, 3), "w4a4_gemm_s4_us_graph": round(t4g * 1e6, 2),
+                          "hipblaslt_bf16_us_graph": round(tbg * 1e6, 2),
+                          "speedup_vs_bf16_graph": round(tbg / t4g, 3)})
         log(f"GEMM alone {M:5d}x{N:5d}x{K}: {t4 * 1e6:8.2f} us | fp16 {th * 1e6:8.2f} | bf16 {tb * 1e6:8.2f} | "
-            f"{th / t4:5.2f}x {tb / t4:5.2f}x")
+            f"{th / t4:5.2f}x {tb / t4:5.2f}x | {gs} per replay: {t4g * 1e6:8.2f} us vs bf16 {tbg * 1e6:8.2f}")
         del copies, blas_w, half_w
         torch.cuda.empty_cache()
     for M, N in REF_E2E_SHAPES:
@@ -269,11 +277,18 @@ def sweep(args):
         t4 = time_med5(capture([make_chain(X, T, wq, ws, M)]), 1, reps)
         tb = time_med5(capture([lambda: torch.matmul(X, blas_w[0].t())]), 1, reps)
         th = time_med5(capture([lambda: torch.matmul(X16, half_w[0].t())]), 1, reps)
+        gs = args.graph_steps
+        r12 = max(1, reps // gs)
+        t4g = time_med5(graph_of(lambda i: make_chain(X, copies[i % len(copies)][2], copies[i % len(copies)][0],
+                                                      copies[i % len(copies)][1], M), gs), gs, r12)
+        tbg = time_med5(graph_of(lambda i: (lambda Wc=blas_w[i % len(blas_w)]: torch.matmul(X, Wc.t())), gs), gs, r12)
         e2e_rows.append({"M": M, "N": N, "K": K, "layer_us": round(t4 * 1e6, 2),
                          "hipblaslt_fp16_us": round(th * 1e6, 2), "hipblaslt_bf16_us": round(tb * 1e6, 2),
-                         "speedup_vs_fp16": round(th / t4, 3), "speedup_vs_bf16": round(tb / t4, 3)})
+                         "speedup_vs_fp16": round(th / t4, 3), "speedup_vs_bf16": round(tb / t4, 3),
+                         "layer_us_graph": round(t4g * 1e6, 2), "hipblaslt_bf16_us_graph": round(tbg * 1e6, 2),
+                         "speedup_vs_bf16_graph": round(tbg / t4g, 3)})
         log(f"layer {M:5d}x{N:5d}x{K}: {t4 * 1e6:8.2f} us | fp16 {th * 1e6:8.2f} | bf16 {tb * 1e6:8.2f} | "
-            f"{th / t4:5.2f}x {tb / t4:5.2f}x")
+            f"{th / t4:5.2f}x {tb / t4:5.2f}x | {gs} per replay: {t4g * 1e6:8.2f} us vs bf16 {tbg * 1e6:8.2f}")
         del copies, blas_w, half_w
         torch.cuda.empty_cache()
     print(json.dumps({"sweep": "reference matrices (bench/exp_p13_official.py, bench/exp_p13_matrix.py)",

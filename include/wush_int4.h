@@ -106,8 +106,10 @@ size_t wush_gemm_s4_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* Group-scaled W4A4 GEMM, any M >= 1, K % 32 == 0: the product of
  * wush_gemv_int4, y (M, N) fp16.  On int8 MFMA with exact int32 group dots,
- * except for prefill shapes (K % 256 == 0, M >= 256, at least 128 workgroups
- * of 256x256 tiles, K split into the workspace from M = 512), which run fp16 MFMA on code*scale operands (exact after a
+ * except for prefill shapes (K % 256 == 0, M >= 256, at least 64 tiles of
+ * 256x256 or N >= 2048, and at least 128 workgroups counting the K slices of
+ * at least 32 groups each that the workspace holds from M = 512), which run
+ * fp16 MFMA on code*scale operands (exact after a
  * power-of-two shift per row and column) accumulated in fp32 over all of K.
  * Both agree with the fp64 product to 2e-3 relative Frobenius (tested); a row
  * or column with a non-finite scale gives NaN there.

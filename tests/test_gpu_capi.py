@@ -578,8 +578,10 @@ def test_gemm_random_shapes_all_paths(capi):
 # Shapes the planner sends to the 256x256 fp16-MFMA tiles (K % 256 == 0,
 # M >= 256, at least 128 tiles): ragged M and N, one and several load batches.
 # The last two split K across workgroups (8 and 4 slices of 8 groups).
+# prefill plans: no K split, and (the last two) ragged M split into 4 and 2
+# slices of 32 groups
 H16_SHAPES = [(512, 32768, 256), (700, 30000, 512), (1030, 16400, 1024), (4096, 4096, 2048), (300, 33000, 512),
-              (600, 4096, 2048), (1030, 4096, 1024)]
+              (600, 4096, 4096), (1030, 4096, 2048)]
 
 
 def _sample(g, n, k):
@@ -624,13 +626,13 @@ def test_gemm_h16_matches_oracle(capi, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K,wide", [(2048, 8192, 4096, False), (300, 33000, 512, False),
-                                         (1030, 16400, 1024, False), (512, 8192, 1024, False),
-                                         (512, 8192, 1024, True), (300, 33000, 512, True)])
+                                         (1030, 16400, 1024, False), (512, 8192, 2048, False),
+                                         (512, 8192, 2048, True), (300, 33000, 512, True)])
 def test_gemm_h16_preconverted_activations_bit_identical(capi, M, N, K, wide):
     # with a workspace of wush_gemm_s4_workspace_bytes, prefill plans with
     # N >= 8192 convert the activations once into it (gemm_h16a); without
     # that room they are converted per tile (gemm_h16w8): the same fp16
-    # operands in the same MFMA order, so the same bits.  (512, 8192, 1024)
+    # operands in the same MFMA order, so the same bits.  (512, 8192, 2048)
     # also splits K (2 slices), compared against the no-alloc entry point,
     # whose scratch holds the partials but not the converted activations.
     import torch

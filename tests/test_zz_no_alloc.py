@@ -76,7 +76,7 @@ def test_noalloc_matches_workspace_entry_point(capi, pair):
 
 def test_noalloc_rejects_plans_beyond_scratch(capi):
     import torch
-    M, N, K = 768, 4096, 4096           # fp16 tiles split K 8 ways: 96 MiB of partials
+    M, N, K = 768, 4096, 8192           # fp16 tiles split K 8 ways (32 groups each): 96 MiB of partials
     need = capi.gemm_s4_workspace_bytes(M, N, K)
     assert need > capi.GEMM_SCRATCH_BYTES
     lib = capi.load()

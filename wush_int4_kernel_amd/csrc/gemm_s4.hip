@@ -685,6 +685,26 @@ static size_t plan_bytes(const Plan& p, int64_t M, int64_t N, int64_t K) {
 #ifndef WUSH_H16_MAX_SPLITS
 #define WUSH_H16_MAX_SPLITS 8
 #endif
+// Every K slice of the fp16 tiles keeps at least this many groups: a slice
+// of 16 groups spends more on its ring fill, prologue and epilogue and on the
+// fp32 partials than on MFMAs (M=2048 N=512 K=4096: 8 slices 41.5 us, 4
+// slices 28.7; K=N=2048 M=1024: 40.8 -> 30.6; M=512 N=2048 K=4096 38.4 ->
+// 30.2; unchanged at 1024 x 4096 x 4096, 512 x 8192 x 8192, 2048 x 4096 x 4096).
+#ifndef WUSH_H16_MIN_SPLIT_GROUPS
+#define WUSH_H16_MIN_SPLIT_GROUPS 32
+#endif
+// With fewer than this many 256x256 tiles and N below WUSH_H16_FEW_TILES_MIN_N
+// the int8 tiles win (K=4096: M=4096 N=512 51.2 -> 46.1 us, M=2048 N=1024
+// 49.0 -> 46.1; K=8192: M=1024 N=1024 50.0 -> 45.1, M=2048 N=512 50.1 ->
+// 46.3); from N = 2048 the fp16 tiles keep them (M=1024 N=2048 K=8192: 64.9
+// against 72.3 us with the int8 tiles), and from 64 tiles at any N (M=4096
+// N=1024 K=4096: 66.6 against 74.9).
+#ifndef WUSH_H16_FEW_TILES
+#define WUSH_H16_FEW_TILES 64
+#endif
+#ifndef WUSH_H16_FEW_TILES_MIN_N
+#define WUSH_H16_FEW_TILES_MIN_N 2048
+#endif
 #ifndef WUSH_H16_SPLIT_MIN_M
 #define WUSH_H16_SPLIT_MIN_M 512
 #endif
@@ -778,12 +798,14 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         p.groups_per_split = (int)gps;
         return p;
     }
-    if (allow_split && K % 256 == 0 && M >= WUSH_H16_MIN_M) {
+    if (allow_split && K % 256 == 0 && M >= WUSH_H16_MIN_M &&
+        (((M + 255) / 256) * ((N + 255) / 256) >= WUSH_H16_FEW_TILES || N >= WUSH_H16_FEW_TILES_MIN_N)) {
         // fp16-MFMA tiles, with K split across workgroups (slices of a
         // multiple of 8 groups) while fewer than 256 workgroups would run
         const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
         int s = 1;
         while (M >= WUSH_H16_SPLIT_MIN_M && s < WUSH_H16_MAX_SPLITS && tiles * s < 256 && G0 % (16 * s) == 0 &&
+               G0 / (2 * s) >= WUSH_H16_MIN_SPLIT_GROUPS &&
                (size_t)(2 * s) * (size_t)M * (size_t)N * sizeof(float) <= ws_bytes_available)
             s *= 2;
         if (tiles * s >= WUSH_H16_MIN_TILES) {
