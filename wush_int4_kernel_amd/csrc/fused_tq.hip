@@ -188,14 +188,31 @@ __global__ __launch_bounds__(256) void fused_tq_rows_kernel(const uint16_t* __re
     const int64_t cb = (int64_t)blockIdx.x * kBlocksPerWg;
     const int64_t r0 = (int64_t)blockIdx.y * kRowsPerWave;
 
+    // tile inside both tensors (workgroup-uniform): wave-uniform bases plus
+    // 32-bit lane offsets (below 8 K + 128 bytes, so K < 2^28 keeps them in
+    // range), no clamping
+    const bool full = r0 + kRowsPerWave <= rows && cb + kBlocksPerWg <= C && K < ((int64_t)1 << 28);
+
     // coalesced input: wavefront w loads rows 16w .. 16w + 15 of the tile
+    if (full) {
+        const global_cptr<uint8_t> xb =
+            uniform_ptr(reinterpret_cast<const uint8_t*>(x + (r0 + 16 * wave) * K + cb * 32));
+        uint32_t lo = ((uint32_t)(lane >> 4) * (uint32_t)K + (uint32_t)(lane & 15) * 8u) * 2u;
+        asm("" : "+v"(lo));                      // keeps the 32-bit lane offset form
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int rl = 16 * wave + 4 * k + (lane >> 4);
-        const int64_t rr = min(r0 + rl, rows - 1);
-        const int64_t cc = min(cb + ((lane & 15) >> 2), C - 1);
-        const uint4 v = *reinterpret_cast<const uint4*>(x + rr * K + cc * 32 + (lane & 3) * 8);
-        *reinterpret_cast<uint4*>(sx + rl * kTqXPitch + (lane & 15) * 16) = v;
+        for (int k = 0; k < 4; ++k) {
+            const u32x4 v = *reinterpret_cast<global_cptr<u32x4>>(xb + (size_t)(8 * k) * (size_t)K + lo);
+            *reinterpret_cast<u32x4*>(sx + (16 * wave + 4 * k + (lane >> 4)) * kTqXPitch + (lane & 15) * 16) = v;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int rl = 16 * wave + 4 * k + (lane >> 4);
+            const int64_t rr = min(r0 + rl, rows - 1);
+            const int64_t cc = min(cb + ((lane & 15) >> 2), C - 1);
+            const uint4 v = *reinterpret_cast<const uint4*>(x + rr * K + cc * 32 + (lane & 3) * 8);
+            *reinterpret_cast<uint4*>(sx + rl * kTqXPitch + (lane & 15) * 16) = v;
+        }
     }
     __syncthreads();
     uint32_t ux[16];
@@ -217,10 +234,22 @@ __global__ __launch_bounds__(256) void fused_tq_rows_kernel(const uint16_t* __re
     // coalesced output: wavefront w stores rows 16w .. 16w + 15, 4 lanes a row
     const int rl = 16 * wave + (lane >> 2);
     const int bl = lane & 3;
-    const int64_t r = r0 + rl, cs = cb + bl;
-    if (r < rows && cs < C) {
-        *reinterpret_cast<uint4*>(q + (r * C + cs) * 16) = *reinterpret_cast<const uint4*>(sq + rl * kTqQPitch + bl * 16);
-        s[r * C + cs] = ss[rl * kBlocksPerWg + bl];
+    const u32x4 qv = *reinterpret_cast<const u32x4*>(sq + rl * kTqQPitch + bl * 16);
+    const uint16_t sv = ss[rl * kBlocksPerWg + bl];
+    if (full) {
+        const int64_t e0 = (r0 + 16 * wave) * C + cb;           // first (row, block) of the wavefront
+        const global_ptr<uint8_t> qb = uniform_wptr(q + e0 * 16);
+        const global_ptr<uint16_t> sp = uniform_wptr(s + e0);
+        uint32_t eo = (uint32_t)(lane >> 2) * (uint32_t)C + (uint32_t)bl;
+        asm("" : "+v"(eo));
+        *reinterpret_cast<global_ptr<u32x4>>(qb + eo * 16u) = qv;
+        sp[eo] = sv;
+    } else {
+        const int64_t r = r0 + rl, cs = cb + bl;
+        if (r < rows && cs < C) {
+            *reinterpret_cast<u32x4*>(q + (r * C + cs) * 16) = qv;
+            s[r * C + cs] = sv;
+        }
     }
 }
 

@@ -133,20 +133,6 @@ template <int M> using XsStage = typename XsStageT<M>::type;
 __device__ __forceinline__ float xs_at(const float* xs_l, int i) { return xs_l[i]; }
 __device__ __forceinline__ float xs_at(const float2* xs_l, int i) { return xs_l[i].x; }
 
-// The pointer as a wave-uniform (SGPR) global-memory pointer: p must be the
-// same in every lane.  Loads from it plus a 32-bit lane offset then use the
-// scalar-base address form with no per-lane 64-bit arithmetic.
-template <typename T>
-using global_cptr = const __attribute__((address_space(1))) T*;
-
-template <typename T>
-__device__ __forceinline__ global_cptr<T> uniform_ptr(const T* p) {
-    const uint64_t a = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-    return reinterpret_cast<global_cptr<T>>(((uint64_t)hi << 32) | lo);
-}
-
 // Stage the activation codes and scales in LDS; for M >= 2 returns whether
 // every sx of the block is in range (block-uniform).
 template <int M>

@@ -42,6 +42,30 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+// The pointer as a wave-uniform (SGPR) global-memory pointer: p must be the
+// same in every lane.  Loads and stores through it plus a 32-bit lane offset
+// then use the scalar-base address form with no per-lane 64-bit arithmetic.
+template <typename T>
+using global_cptr = const __attribute__((address_space(1))) T*;
+template <typename T>
+using global_ptr = __attribute__((address_space(1))) T*;
+
+template <typename T>
+__device__ __forceinline__ global_cptr<T> uniform_ptr(const T* p) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return reinterpret_cast<global_cptr<T>>(((uint64_t)hi << 32) | lo);
+}
+
+template <typename T>
+__device__ __forceinline__ global_ptr<T> uniform_wptr(T* p) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return reinterpret_cast<global_ptr<T>>(((uint64_t)hi << 32) | lo);
+}
+
 // Group scale from the two sequential sums (rtn_int4.py:39-48):
 // mean = s1/32, var = s2/32 - mean*mean, scale = sqrt(var)*C + 1e-8 if
 // var >= 0 else 1.0; returns the bf16 bits, *sf gets the bf16 value.
