@@ -503,7 +503,9 @@ def main():
     Xc2 = acts_c(Mc).to(torch.bfloat16)
     Wc2 = torch.randn(Kc, Kc, generator=gc, device=dev, dtype=torch.float32) * 0.02
     Tc2 = compute_wush_transform(acts_c(512).double(), Wc2.double()).to(torch.bfloat16).contiguous()
-    t = time_med5(capture([lambda: _C.fused_transform_quant_int4(Xc2, Tc2)] * 10), 10, 4)
+    # 40 calls per graph replay, as the layer steps: a replay costs about 10 us
+    # beyond its kernels on this part, 1 us per call at 10 calls
+    t = time_med5(capture([lambda: _C.fused_transform_quant_int4(Xc2, Tc2)] * 40), 40, 1)
     tq_bytes = 2 * Mc * Kc + 64 * Kc + Mc * Kc // 2 + Mc * Kc // 16
     tq_macs = 32 * Mc * Kc              # 32 MACs per element, on the fp32 matrix cores
     ops["fused_tq_cfg2"] = {
