@@ -144,3 +144,18 @@ def test_reference_python_modules_exposed():
     s = torch.tensor([[0.5]], dtype=torch.bfloat16)
     d = rtn_int4.dequant_int4(q, s)
     assert d.shape == (1, 32) and d[0, 0].item() == 1.5 and d[0, 1].item() == -1.5
+
+
+def test_tuning_defines_parsing(monkeypatch):
+    # WUSH_DEFINES becomes -D flags on the hipcc lines; only WUSH_* names with
+    # plain values pass, so the variable cannot smuggle other compiler flags in
+    from wush_int4_kernel_amd import _build
+
+    monkeypatch.setenv("WUSH_DEFINES", "WUSH_TQ_ROWS_LDS_PAD=0  WUSH_GEMV_WAVES=8 WUSH_X")
+    assert _build.tuning_defines() == ["-DWUSH_TQ_ROWS_LDS_PAD=0", "-DWUSH_GEMV_WAVES=8", "-DWUSH_X"]
+    monkeypatch.delenv("WUSH_DEFINES")
+    assert _build.tuning_defines() == []
+    for bad in ("-fsanitize=address", "WUSH_A=1;rm", "OTHER=1", "WUSH_A=$(x)", "wush_a=1"):
+        monkeypatch.setenv("WUSH_DEFINES", bad)
+        with pytest.raises(ValueError):
+            _build.tuning_defines()

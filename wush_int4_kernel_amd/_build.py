@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import subprocess
 import sys
 import sysconfig
@@ -67,13 +68,27 @@ def hipcc() -> str:
     return "hipcc"
 
 
+def tuning_defines() -> list:
+    """-D flags for the build-time tuning macros of csrc/*.hip, from the
+    WUSH_DEFINES environment variable ("WUSH_TQ_ROWS_LDS_PAD=0 WUSH_GEMV_WAVES=8").
+    Only WUSH_* names with plain values are accepted; anything else is an error."""
+    flags = []
+    for item in os.environ.get("WUSH_DEFINES", "").split():
+        name, eq, value = item.partition("=")
+        if not re.fullmatch(r"WUSH_[A-Z0-9_]+", name) or not re.fullmatch(r"[0-9A-Za-z_]*", value):
+            raise ValueError(f"WUSH_DEFINES: {item!r} is not WUSH_NAME or WUSH_NAME=value")
+        flags.append(f"-D{name}{eq}{value}")
+    return flags
+
+
 def build_capi(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     cc = hipcc()
 
     def compile_one(src):
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-        _run([cc, *source_flags(src), f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj], verbose)
+        _run([cc, *source_flags(src), *tuning_defines(), f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj],
+             verbose)
         return obj
 
     with cf.ThreadPoolExecutor(max_workers=min(6, len(HIP_SOURCES))) as ex:
