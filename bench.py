@@ -515,7 +515,8 @@ def main():
         "fp32_macs": tq_macs, "mfma_f32_frac": round(2 * tq_macs / t / (F32_MFMA_PEAK_TFLOPS * 1e12), 4),
     }
     # a2/a3: quant_int4 of one Llama-70B weight tensor (N x K bf16), HBM-bound
-    t = time_med5(capture([lambda: _C.quant_int4(Wt)] * 2), 2, 2)
+    # 8 calls per replay (1.2 GB each): the replay's own cost spread as in the other op timings
+    t = time_med5(capture([lambda: _C.quant_int4(Wt)] * 8), 8, 1)
     q_bytes = N * K * 2 + N * K // 2 + N * K // 16
     ops["quant_int4_l70_weights"] = {
         "us": round(t * 1e6, 2), "shape": f"{N}x{K} bf16", "hbm_bytes": q_bytes,
