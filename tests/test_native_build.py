@@ -151,8 +151,8 @@ def test_tuning_defines_parsing(monkeypatch):
     # plain values pass, so the variable cannot smuggle other compiler flags in
     from wush_int4_kernel_amd import _build
 
-    monkeypatch.setenv("WUSH_DEFINES", "WUSH_TQ_ROWS_LDS_PAD=0  WUSH_GEMV_WAVES=8 WUSH_X")
-    assert _build.tuning_defines() == ["-DWUSH_TQ_ROWS_LDS_PAD=0", "-DWUSH_GEMV_WAVES=8", "-DWUSH_X"]
+    monkeypatch.setenv("WUSH_DEFINES", "WUSH_TQ_SMALLM_PAIRS=0  WUSH_GEMV_WAVES=8 WUSH_X")
+    assert _build.tuning_defines() == ["-DWUSH_TQ_SMALLM_PAIRS=0", "-DWUSH_GEMV_WAVES=8", "-DWUSH_X"]
     monkeypatch.delenv("WUSH_DEFINES")
     assert _build.tuning_defines() == []
     for bad in ("-fsanitize=address", "WUSH_A=1;rm", "OTHER=1", "WUSH_A=$(x)", "wush_a=1"):

@@ -70,7 +70,7 @@ def hipcc() -> str:
 
 def tuning_defines() -> list:
     """-D flags for the build-time tuning macros of csrc/*.hip, from the
-    WUSH_DEFINES environment variable ("WUSH_TQ_ROWS_LDS_PAD=0 WUSH_GEMV_WAVES=8").
+    WUSH_DEFINES environment variable ("WUSH_TQ_SMALLM_PAIRS=8192 WUSH_GEMV_WAVES=8").
     Only WUSH_* names with plain values are accepted; anything else is an error."""
     flags = []
     for item in os.environ.get("WUSH_DEFINES", "").split():

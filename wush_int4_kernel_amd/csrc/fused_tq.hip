@@ -309,16 +309,6 @@ __global__ __launch_bounds__(64) void fused_tq_smallm_kernel(const uint16_t* __r
 #ifndef WUSH_TQ_SMALLM_PAIRS
 #define WUSH_TQ_SMALLM_PAIRS 16384
 #endif
-// Unused dynamic LDS per rows-kernel workgroup: with its 22.5 KiB of static
-// LDS, 3 workgroups fit in a CU's 160 KiB instead of 5 (VGPR-bound).  When
-// every workgroup of a launch is resident at once, all load their input at
-// the same moment and only then compute; with fewer resident, later
-// workgroups load while earlier ones compute.  2048 x 4096: 13.0 -> 12.0 us;
-// 4096 x 8192 38.4 -> 37.8; 16384 x 4096 unchanged; inputs outside the MFMA
-// range (the fma loops need the occupancy) 10% slower.  Bit-identical.
-#ifndef WUSH_TQ_ROWS_LDS_PAD
-#define WUSH_TQ_ROWS_LDS_PAD 24576
-#endif
 extern "C" int wush_fused_tq(const uint16_t* x, const uint16_t* t, uint8_t* q, uint16_t* s,
                              int64_t rows, int64_t K, hipStream_t stream) {
     WUSH_REQUIRE(rows >= 0 && K > 0 && K % 32 == 0);
@@ -336,7 +326,7 @@ extern "C" int wush_fused_tq(const uint16_t* x, const uint16_t* t, uint8_t* q, u
         const int64_t gy = (rows + wush::kRowsPerWave - 1) / wush::kRowsPerWave;
         WUSH_REQUIRE(gx <= 0x7fffffffLL && gy <= 65535);
         const dim3 grid((unsigned)gx, (unsigned)gy);
-        wush::fused_tq_rows_kernel<<<grid, 256, WUSH_TQ_ROWS_LDS_PAD, stream>>>(x, t, q, s, rows, K);
+        wush::fused_tq_rows_kernel<<<grid, 256, 0, stream>>>(x, t, q, s, rows, K);
     }
     return (int)hipGetLastError();
 }
