@@ -88,14 +88,23 @@ int wush_fused_tq_transform32(const uint16_t *x, const uint16_t *t, float *xp, i
 
 /* Decode GEMV for 1 <= M <= 8: y[m][n] = sum_g sx[m][g]*sw[n][g]*D[m][n][g]
  * with D the exact int32 dot of group g.  xq: M*K/2; xs: M*K/32; wq: N*K/2;
- * ws: N*K/32; y: M*N fp16.  The activations must fit 64 KiB of LDS
- * (M*K/2 + M*K/4 bytes), except at M = 7, 8 with K a multiple of 2048 in
- * [8192, 32768] and N > 32768, which keep them in registers; other shapes
+ * ws: N*K/32; y: M*N fp16.  Shapes that wush_gemv_int4_supported rejects
  * return hipErrorInvalidValue (wush_gemm_s4 takes any shape).
  * Replaces w4a4_gemv (csrc/gemv_int4.cu:191-223, M == 1) and w4a4_gemv_multi
  * (csrc/gemv_int4.cu:145-189, M <= 8). */
 int wush_gemv_int4(const uint8_t *xq, const uint16_t *xs, const uint8_t *wq, const uint16_t *ws,
                    uint16_t *y, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* 1 if wush_gemv_int4 runs (M, N, K), else 0.  The rule depends on the
+ * library's build (its tuning macros): 1 <= M <= 8, K % 32 == 0, and either
+ * the activations fit the staged kernel's 64 KiB of LDS (M*K/2 + M*K/4
+ * bytes) or the shape is one of the K-split kernel's (by default M = 7, 8,
+ * K a multiple of 2048 in [8192, 32768], N > 32768), which keeps them in
+ * registers.  A host that routes products between wush_gemv_int4 and
+ * wush_gemm_s4 asks this instead of restating the rule.  The reference has
+ * no counterpart: its w4a4_gemv_multi checks M <= 8 and fails at launch when
+ * its shared memory does not fit (csrc/gemv_int4.cu:160-169). */
+int wush_gemv_int4_supported(int64_t M, int64_t N, int64_t K);
 
 /* Bytes of workspace wush_gemm_s4 uses for (M, N, K); 0 when it needs none:
  * fp32 split-K partials, and for prefill shapes with N >= 8192 the
@@ -124,17 +133,18 @@ int wush_gemm_s4(const uint8_t *xq, const uint16_t *xs, const uint8_t *wq, const
  * array per device, held from the library's load until the process ends. */
 #define WUSH_GEMM_SCRATCH_BYTES (64u << 20)
 
-/* Status of wush_gemm_s4_noalloc when the shape's split-K plan needs more than
- * WUSH_GEMM_SCRATCH_BYTES (wush_error_string explains it). */
+/* Status of wush_gemm_s4_noalloc if no plan of the shape fits
+ * WUSH_GEMM_SCRATCH_BYTES (wush_error_string explains it).  The planner
+ * always has one (a single K slice needs no scratch), so this is a guard. */
 #define WUSH_ERROR_SCRATCH_TOO_SMALL 0x57550001
 
 /* wush_gemm_s4 that allocates nothing and takes no workspace: its split-K
  * partials (if the plan splits K) go to the library's static scratch of
- * WUSH_GEMM_SCRATCH_BYTES on the current device.  The same results as
- * wush_gemm_s4, bit for bit, with the same split of K; prefill shapes convert
- * their activations per tile instead of into the workspace.  A shape whose
- * partials need more than the scratch returns WUSH_ERROR_SCRATCH_TOO_SMALL
- * and launches nothing.  Nothing needs clearing
+ * WUSH_GEMM_SCRATCH_BYTES on the current device.  The plan is the one
+ * wush_gemm_s4 chooses when given a workspace of WUSH_GEMM_SCRATCH_BYTES,
+ * and the results are those of that call, bit for bit: a shape whose full
+ * split of K would need more partials than the scratch holds is split into
+ * fewer slices.  Nothing needs clearing
  * between calls: every partial is written before it is summed.  All calls on
  * one device share its scratch, so calls that overlap on one device (on
  * different streams, or from different host threads without ordering) race.

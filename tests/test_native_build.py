@@ -41,7 +41,8 @@ def test_header_declares_expected_entry_points():
     syms = declared_symbols()
     for s in ["wush_quant_int4", "wush_fused_tq", "wush_gemv_int4", "wush_gemm_s4",
               "wush_gemm_s4_workspace_bytes", "wush_mfma_selftest", "wush_quant_int4_tensor_scale",
-              "wush_gemm_s4_tensor_scale", "wush_abi_version", "wush_error_string"]:
+              "wush_gemm_s4_tensor_scale", "wush_abi_version", "wush_error_string",
+              "wush_gemv_int4_supported"]:
         assert s in syms, s
 
 
@@ -159,3 +160,45 @@ def test_tuning_defines_parsing(monkeypatch):
         monkeypatch.setenv("WUSH_DEFINES", bad)
         with pytest.raises(ValueError):
             _build.tuning_defines()
+
+
+# (M, N, K) on both sides of every term of the GEMV shape rule: the staged
+# kernel's 64 KiB LDS limit, the K-split kernel's M, N and K bounds
+GEMV_RULE_SHAPES = [(M, N, K) for M in (1, 4, 6, 7, 8, 9) for N in (4096, 32768, 32769, 57344)
+                    for K in (4096, 8192, 16384, 32768, 34816, 65536)] + [(0, 4096, 4096), (8, 57344, 8200)]
+
+
+def _check_gemv_rule(lib):
+    """wush_gemv_int4 rejects (before touching a device) exactly the shapes
+    wush_gemv_int4_supported reports as unsupported; returns the supported set."""
+    P = ctypes.c_void_p
+    lib.wush_gemv_int4_supported.argtypes = [ctypes.c_int64] * 3
+    lib.wush_gemv_int4.argtypes = [P] * 5 + [ctypes.c_int64] * 3 + [P]
+    ok = set()
+    for M, N, K in GEMV_RULE_SHAPES:
+        sup = lib.wush_gemv_int4_supported(M, N, K)
+        st = lib.wush_gemv_int4(P(16), P(16), P(16), P(16), P(16), M, N, K, None)
+        assert sup in (0, 1)
+        assert (st == INVALID) == (sup == 0), (M, N, K, sup, st)
+        if sup:
+            ok.add((M, N, K))
+    return ok
+
+
+def test_gemv_rule_is_the_librarys(capi, tmp_path):
+    # The _C product ops route to wush_gemv_int4 only where the library says
+    # it runs the shape (bindings.cpp asks wush_gemv_int4_supported), so a
+    # build with other tuning macros cannot send a shape the GEMV rejects.
+    # Default build: the K-split kernel takes M = 7, 8 at L70 and K = 16384.
+    default = _check_gemv_rule(capi.load())
+    assert (8, 57344, 8192) in default and (8, 57344, 16384) in default and (7, 32769, 32768) in default
+    assert (8, 32768, 16384) not in default and (6, 57344, 16384) not in default
+    assert (1, 4096, 65536) in default and (4, 4096, 16384) in default and (6, 4096, 16384) not in default
+    # A build with the K-split kernel off (WUSH_GEMV_KS_MIN_M=9, the documented
+    # off value) keeps only the LDS-staged shapes.
+    from wush_int4_kernel_amd import _build
+    lib_path = str(tmp_path / "libwush_int4_ks_off.so")
+    _build.build_capi(lib_path=lib_path, build_dir=str(tmp_path / "obj"), defines="WUSH_GEMV_KS_MIN_M=9")
+    off = _check_gemv_rule(ctypes.CDLL(lib_path))
+    assert (8, 57344, 16384) not in off and (7, 57344, 32768) not in off and (7, 57344, 8192) in off
+    assert off == {s for s in default if s[0] * (s[2] // 2) + s[0] * (s[2] // 32) * 8 <= 64 * 1024}

@@ -68,12 +68,13 @@ def hipcc() -> str:
     return "hipcc"
 
 
-def tuning_defines() -> list:
-    """-D flags for the build-time tuning macros of csrc/*.hip, from the
-    WUSH_DEFINES environment variable ("WUSH_TQ_SMALLM_PAIRS=8192 WUSH_GEMV_WAVES=8").
+def tuning_defines(spec: str | None = None) -> list:
+    """-D flags for the build-time tuning macros of csrc/*.hip, from ``spec``
+    or else the WUSH_DEFINES environment variable
+    ("WUSH_TQ_SMALLM_PAIRS=8192 WUSH_GEMV_WAVES=8").
     Only WUSH_* names with plain values are accepted; anything else is an error."""
     flags = []
-    for item in os.environ.get("WUSH_DEFINES", "").split():
+    for item in (os.environ.get("WUSH_DEFINES", "") if spec is None else spec).split():
         name, eq, value = item.partition("=")
         if not re.fullmatch(r"WUSH_[A-Z0-9_]+", name) or not re.fullmatch(r"[0-9A-Za-z_]*", value):
             raise ValueError(f"WUSH_DEFINES: {item!r} is not WUSH_NAME or WUSH_NAME=value")
@@ -81,22 +82,26 @@ def tuning_defines() -> list:
     return flags
 
 
-def build_capi(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
+def build_capi(verbose: bool = False, lib_path: str = LIB, build_dir: str = BUILD,
+               defines: str | None = None) -> str:
+    """Compile libwush_int4.so (to ``lib_path``, objects in ``build_dir``) with
+    the tuning macros of ``defines`` (default: the WUSH_DEFINES variable)."""
+    os.makedirs(build_dir, exist_ok=True)
     cc = hipcc()
+    dflags = tuning_defines(defines)
 
     def compile_one(src):
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-        _run([cc, *source_flags(src), *tuning_defines(), f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj],
+        obj = os.path.join(build_dir, src.replace(".hip", ".o"))
+        _run([cc, *source_flags(src), *dflags, f"-I{INCLUDE}", "-c", os.path.join(CSRC, src), "-o", obj],
              verbose)
         return obj
 
     with cf.ThreadPoolExecutor(max_workers=min(6, len(HIP_SOURCES))) as ex:
         objs = list(ex.map(compile_one, HIP_SOURCES))
-    tmp = LIB + ".tmp"
+    tmp = lib_path + ".tmp"
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib_path)
+    return lib_path
 
 
 def build_torch_ext(verbose: bool = False) -> str:

@@ -23,6 +23,7 @@ SIGNATURES = {
     "wush_fused_tq": ([_P, _P, _P, _P, _I64, _I64, _P], _I),
     "wush_fused_tq_transform32": ([_P, _P, _P, _I64, _P], _I),
     "wush_gemv_int4": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P], _I),
+    "wush_gemv_int4_supported": ([_I64, _I64, _I64], _I),
     "wush_gemm_s4_workspace_bytes": ([_I64, _I64, _I64], _SZ),
     "wush_gemm_s4": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ, _P], _I),
     "wush_gemm_s4_noalloc": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P], _I),
@@ -71,6 +72,10 @@ def fused_tq(x_ptr, t_ptr, q_ptr, s_ptr, rows, K, stream) -> None:
 
 def gemv_int4(xq, xs, wq, ws, y, M, N, K, stream) -> None:
     _check(load().wush_gemv_int4(xq, xs, wq, ws, y, M, N, K, stream), "wush_gemv_int4")
+
+
+def gemv_int4_supported(M, N, K) -> bool:
+    return bool(load().wush_gemv_int4_supported(M, N, K))
 
 
 def gemm_s4_workspace_bytes(M, N, K) -> int:

@@ -110,16 +110,12 @@ void check_packed(const torch::Tensor& xq, const torch::Tensor& xs, const torch:
 // the Llama-70B FFN weights (K=8192 N=57344 M=8: 51.8 vs 55.4 us); the
 // K-split int8-MFMA streaming GEMM (wush_gemm_s4) is faster at 5 <= M <= 8
 // when N <= 24576 (K=N=4096 M=8: 5.8 vs 7.2 us; K=N=8192 M=8: 11.9 vs
-// 13.3 us; K=4096 N=24576 M=8: 14.3 vs 15.0 us).  The staged GEMV keeps
-// M*K*(1/2 + 1/4) bytes of activation codes and scale terms in LDS, at most
-// 64 KiB; at M = 7, 8 with K a multiple of 2048 in [8192, 32768] and
-// N > 32768 the GEMV's K-split kernel keeps them in registers instead and
-// takes any such K (K=16384 N=57344 M=8: 90 vs 117 us for the GEMM; K=32768
-// N=33000: 130 vs 141 us), the shape rule of wush_gemv_int4.
+// 13.3 us; K=4096 N=24576 M=8: 14.3 vs 15.0 us).  Which shapes the GEMV
+// takes at all (its LDS staging limit, and the K-split kernel's shapes) is
+// the library's rule, which its build-time tuning macros change, so it is
+// asked, not restated here.
 bool gemv_preferred(int64_t M, int64_t N, int64_t K) {
-    const bool lds_fits = M * (K / 2) + M * (K / 32) * 8 <= 64 * 1024;
-    const bool ksplit = M >= 7 && M <= 8 && N > 32768 && K % 2048 == 0 && K >= 8192 && K <= 32768;
-    return ksplit || (lds_fits && M >= 1 && M <= 8 && (M <= 4 || N > 32768));
+    return wush_gemv_int4_supported(M, N, K) != 0 && (M <= 4 || N > 32768);
 }
 
 // Shared product launch: y (M, N) fp16 = group-scaled product.

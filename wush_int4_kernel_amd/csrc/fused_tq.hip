@@ -317,9 +317,11 @@ extern "C" int wush_fused_tq(const uint16_t* x, const uint16_t* t, uint8_t* q, u
     WUSH_REQUIRE(((uintptr_t)x & 15u) == 0 && ((uintptr_t)t & 15u) == 0 &&
                  ((uintptr_t)q & 15u) == 0 && ((uintptr_t)s & 1u) == 0);
     const int64_t C = K / 32;
-    if (rows * C <= WUSH_TQ_SMALLM_PAIRS) {
+    // the small-M grid holds the rows in grid.y (at most 65535), so any
+    // value of the tuning macro leaves larger launches to the rows kernel
+    if (rows * C <= WUSH_TQ_SMALLM_PAIRS && rows <= 65535) {
         const int64_t gx = (C + wush::kPairsPerWg - 1) / wush::kPairsPerWg;
-        WUSH_REQUIRE(gx <= 0x7fffffffLL && rows <= 65535);
+        WUSH_REQUIRE(gx <= 0x7fffffffLL);
         wush::fused_tq_smallm_kernel<<<dim3((unsigned)gx, (unsigned)rows), 64, 0, stream>>>(x, t, q, s, rows, K);
     } else {
         const int64_t gx = (C + wush::kBlocksPerWg - 1) / wush::kBlocksPerWg;

@@ -984,17 +984,21 @@ int wush_gemm_s4_noalloc(const uint8_t* xq, const uint16_t* xs, const uint8_t* w
     WUSH_REQUIRE(xq && xs && wq && ws && y);
     WUSH_REQUIRE(((uintptr_t)xq & 15u) == 0 && ((uintptr_t)wq & 15u) == 0);
     WUSH_REQUIRE(((uintptr_t)xs & 1u) == 0 && ((uintptr_t)ws & 1u) == 0 && ((uintptr_t)y & 1u) == 0);
-    // the plan wush_gemm_s4 runs with a workspace for its split-K partials
-    // only (no pre-converted activations, whose M*K*2 bytes would not fit);
-    // the partials go to this device's scratch
-    const size_t need = wush::plan_bytes(wush::make_plan(M, N, K, (size_t)-1, true, true, false), M, N, K);
-    if (need > (size_t)WUSH_GEMM_SCRATCH_BYTES) return WUSH_ERROR_SCRATCH_TOO_SMALL;
+    // the plan wush_gemm_s4 runs when its workspace is the scratch's size:
+    // split-K partials only (no pre-converted activations), with fewer K
+    // slices where the shape's full split would need more than the scratch
+    // (one slice needs none, so every shape has such a plan)
+    const bool scales16 = ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws)) & 15u) == 0;
+    const size_t cap = (size_t)WUSH_GEMM_SCRATCH_BYTES;
+    const size_t need = wush::plan_bytes(wush::make_plan(M, N, K, cap, true, scales16, false), M, N, K);
+    if (need > cap) return WUSH_ERROR_SCRATCH_TOO_SMALL;
     int dev = 0;
     const int st = wush::device_setup(&dev);
     if (st != 0) return st;
     void* scratch = need ? wush::scratch_address(dev) : nullptr;
     if (need && scratch == nullptr) return (int)hipErrorInvalidSymbol;
-    return wush::run_gemm<false>(xq, xs, wq, ws, y, M, N, K, scratch, need, 1.0f, nullptr, stream, false);
+    return wush::run_gemm<false>(xq, xs, wq, ws, y, M, N, K, scratch, need ? cap : 0, 1.0f, nullptr, stream,
+                                 false);
 }
 
 int wush_gemm_s4_tensor_scale(const uint8_t* xq, const uint8_t* wq, uint16_t* y, int64_t M, int64_t N,

@@ -565,7 +565,23 @@ static void launch_gemv(const GemvDeviceInfo& info, const uint8_t* xq, const uin
         launch_gemv_t<M, 0>(info, xq, xs, wq, ws, y, N, K, stream);
 }
 
+namespace {
+// The shapes wush_gemv_int4 runs: 1 <= M <= 8 and K % 32 == 0, with the
+// staged kernel's activations (M*K/2 code bytes + M*K/32 pairs of fp32
+// scale terms) in 64 KiB of LDS, or a shape of the K-split kernel (which
+// stages nothing) at M >= kGemvKsMinM.  Both depend on the build's tuning
+// macros, so callers ask the library (wush_gemv_int4_supported).
+bool gemv_shape_supported(int64_t M, int64_t N, int64_t K) {
+    if (M < 1 || M > 8 || N < 0 || K <= 0 || K % 32 != 0 || N > 0x7fffffffLL || K > 0x7fffffffLL) return false;
+    const bool ksplit = M >= kGemvKsMinM && gemv_ks_shape(N, K);
+    return ksplit || (size_t)M * (K / 2) + (size_t)M * (K / 32) * 8 <= 64 * 1024;
+}
+}  // namespace
 }  // namespace wush
+
+extern "C" int wush_gemv_int4_supported(int64_t M, int64_t N, int64_t K) {
+    return wush::gemv_shape_supported(M, N, K) ? 1 : 0;
+}
 
 extern "C" int wush_gemv_int4(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq,
                               const uint16_t* ws, uint16_t* y, int64_t M, int64_t N, int64_t K,
@@ -576,10 +592,7 @@ extern "C" int wush_gemv_int4(const uint8_t* xq, const uint16_t* xs, const uint8
     WUSH_REQUIRE(xq && xs && wq && ws && y);
     WUSH_REQUIRE(((uintptr_t)xq & 15u) == 0 && ((uintptr_t)wq & 15u) == 0);
     WUSH_REQUIRE(((uintptr_t)xs & 1u) == 0 && ((uintptr_t)ws & 1u) == 0 && ((uintptr_t)y & 1u) == 0);
-    // The staged kernel's LDS holds M*K/2 code bytes + M*K/32 pairs of fp32
-    // scale terms; the K-split kernel (M >= 7 on its shapes) stages nothing.
-    const bool ksplit = M >= wush::kGemvKsMinM && wush::gemv_ks_shape(N, K);
-    WUSH_REQUIRE(ksplit || (size_t)M * (K / 2) + (size_t)M * (K / 32) * 8 <= 64 * 1024);
+    WUSH_REQUIRE(wush::gemv_shape_supported(M, N, K));
     int dev = 0;
     const int st = wush::device_setup(&dev);
     if (st != 0) return st;
