@@ -72,3 +72,37 @@ def rel_fro(y: np.ndarray, ref: np.ndarray) -> float:
     num = np.linalg.norm((y - ref).ravel())
     den = np.linalg.norm(ref.ravel())
     return float(num / den) if den > 0 else float(num)
+
+
+def product_check(y: np.ndarray, xq, xs, wq, ws, n_terms: int, chunk: int = 4096):
+    """Whole-output check of a W4A4 product y (M, N) against the fp64 value of
+    dequant(xq, xs) @ dequant(wq, ws)^T (the oracle's dequantization, summed in
+    fp64 over weight-row chunks).
+
+    Returns (relative Frobenius error, worst ratio of |y - ref| to the
+    per-element bound 2^-11 |ref| + 1.01 * n_terms * 2^-24 * (|X| @ |W|^T) +
+    2^-25): the fp16 output rounding plus an fp32 summation of at most n_terms
+    rounded additions of exact terms, plus half of fp16's smallest subnormal.
+    The Frobenius gate alone could hide one wrong column among tens of
+    thousands; the bound holds for every output of a correct product."""
+    import oracle
+    xq = np.ascontiguousarray(xq).reshape(-1, xq.shape[-1])
+    M, N = xq.shape[0], wq.shape[0]
+    assert y.shape == (M, N), (y.shape, M, N)
+    X = oracle.dequant(xq, np.ascontiguousarray(xs).reshape(M, -1)).astype(np.float64)
+    Xa = np.abs(X)
+    num = den = 0.0
+    worst = 0.0
+    for c0 in range(0, N, chunk):
+        c1 = min(N, c0 + chunk)
+        W = oracle.dequant(wq[c0:c1], ws[c0:c1]).astype(np.float64)
+        ref = X @ W.T
+        A = Xa @ np.abs(W).T
+        yy = y[:, c0:c1]
+        assert np.isfinite(yy).all() or not np.isfinite(ref).all(), "non-finite output"
+        d = np.abs(yy - ref)
+        num += float((d * d).sum())
+        den += float((ref * ref).sum())
+        bound = 2.0 ** -11 * np.abs(ref) + 1.01 * n_terms * 2.0 ** -24 * A + 2.0 ** -25
+        worst = max(worst, float((d / bound).max()))
+    return (num / den) ** 0.5 if den > 0 else num ** 0.5, worst

@@ -1,15 +1,20 @@
 """GPU parity at the sizes of every BASELINE.json config, through my_int4._C and
 my_int4.chain as a caller of the reference would use them.
 
-Where the CPU oracle finishes in seconds the whole output is compared; at the
-Llama-70B and prefill sizes the GPU computes everything and seeded samples of
-rows / columns are compared (codes and scales bit-exact, fp16 products within
-2e-3 relative Frobenius of the fp64 dequantized product)."""
+Whole outputs are compared: every code byte and bf16 scale of the weight and
+activation quantizations (bit-exact), and every output of the fp16 products
+against the fp64 dequantized product -- within 2e-3 relative Frobenius, and
+each output within its own rounding bound (tests/_util.product_check), so a
+wrong column cannot hide in the norm.  The one exception is the Llama-70B
+prefill product (4096 x 57344 x 8192), whose fp64 reference would take
+minutes on the host: there two whole 256-row stripes of the output (an
+interior one and the last) are compared, while its weight and activation
+codes are still compared whole."""
 import numpy as np
 import pytest
 
 import oracle
-from _util import (bf16_tensor_bits, f16_tensor_f64, f32_to_bf16_bits, outlier_activations, rel_fro, rng,
+from _util import (bf16_tensor_bits, f16_tensor_f64, f32_to_bf16_bits, outlier_activations, product_check, rng,
                    to_dev_bf16)
 
 pytestmark = pytest.mark.gpu
@@ -31,13 +36,6 @@ def _dev_weights(N, K, seed):
     return W
 
 
-def _check_weight_rows(C, W, wq, ws, rows):
-    Wb = bf16_tensor_bits(W[rows])
-    qo, so = oracle.quant(Wb, "bf16")
-    assert np.array_equal(wq[rows].cpu().numpy(), qo)
-    assert np.array_equal(bf16_tensor_bits(ws[rows]), so)
-
-
 def test_cfg1_cpu_reference_shape(C):
     # X fp16 16x4096 (1% outlier channels x50), W fp16 4096x4096 ~ N(0, 0.02)
     import torch
@@ -53,8 +51,9 @@ def test_cfg1_cpu_reference_shape(C):
     qo, so = oracle.quant(W.cpu().numpy().view(np.uint16), "f16")
     assert np.array_equal(wq.cpu().numpy(), qo) and np.array_equal(bf16_tensor_bits(ws), so)
     y = C.w4a4_gemm_s4(xq, xs, wq, ws)
-    ref = oracle.gemm_f64(xq.cpu().numpy(), bf16_tensor_bits(xs), wq.cpu().numpy(), bf16_tensor_bits(ws))
-    assert rel_fro(f16_tensor_f64(y), ref) < FRO_TOL
+    err, worst = product_check(f16_tensor_f64(y), xq.cpu().numpy(), bf16_tensor_bits(xs), wq.cpu().numpy(),
+                               bf16_tensor_bits(ws), n_terms_for(M, K))
+    assert err < FRO_TOL and worst <= 1.0, (err, worst)
 
 
 def test_cfg2_fused_transform_quant(C):
@@ -81,47 +80,79 @@ def bf16_bits_to_f32_np(b):
     return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
-def _chain_case(C, M, N, K, seed, n_rows_checked, n_cols_checked):
-    """Full layer through my_int4.chain at (M, N, K); check sampled outputs."""
-    import torch
-    from my_int4.chain import make_chain
-    g = rng(seed)
+def n_terms_for(M, K):
+    """Rounded additions per output of the kernel that runs the product:
+    the fp16-MFMA prefill tiles (M >= 256) accumulate all K exact products in
+    fp32 (counted twice, for the MFMA's internal adds); the int8 kernels and
+    the GEMV fold K/32 exact group terms, plus at most 64 partial-sum
+    additions across lanes, wavefronts and K slices."""
+    return 2 * K if M >= 256 else K // 32 + 64
+
+
+def _full_weights(C, N, K, seed):
+    """Weights generated and quantized on the GPU (_C.quant_int4); every code
+    byte and scale is compared with the oracle's quantization of the same
+    bf16 values.  Returns the device tensors and the oracle's arrays."""
     W = _dev_weights(N, K, seed)
     wq, ws = C.quant_int4(W)
+    Wb = bf16_tensor_bits(W)
+    del W
+    qo, so = oracle.quant(Wb, "bf16")
+    del Wb
+    assert np.array_equal(wq.cpu().numpy(), qo), ("weight codes", N, K)
+    assert np.array_equal(bf16_tensor_bits(ws), so), ("weight scales", N, K)
+    return wq, ws, qo, so
+
+
+def _chain_case(C, M, N, K, seed, stripes=None):
+    """Full layer through my_int4.chain at (M, N, K).  Every weight and
+    activation code and scale is compared bit for bit; the product on every
+    row (or on the given 256-row stripes) and every column."""
+    import torch
+    from my_int4.chain import make_chain, route
+    print(f"[cfg] M={M} N={N} K={K} seed={seed}", flush=True)
+    g = rng(seed)
+    wq, ws, qo, so = _full_weights(C, N, K, seed)
     xb = outlier_activations(g, M, K)
     tb = f32_to_bf16_bits(g.standard_normal((K // 32, 32, 32)) * 0.25)
     X, T = to_dev_bf16(xb), to_dev_bf16(tb)
     y = make_chain(X, T, wq, ws, M)()
+    # the transform + quant op the chain ran, compared whole
+    xq, xs = getattr(C, route(M)[0])(X, T)
     torch.cuda.synchronize()
     y = y.reshape(M, N)
-    rows = np.sort(g.choice(M, size=min(M, n_rows_checked), replace=False))
-    cols = np.sort(g.choice(N, size=min(N, n_cols_checked), replace=False))
-    _check_weight_rows(C, W, wq, ws, torch.from_numpy(cols).cuda())
-    qo, so = oracle.fused_tq(xb[rows], tb)
-    wq_s = wq[torch.from_numpy(cols).cuda()].cpu().numpy()
-    ws_s = bf16_tensor_bits(ws[torch.from_numpy(cols).cuda()])
-    ref = oracle.gemm_f64(qo, so, wq_s, ws_s)
-    got = f16_tensor_f64(y[torch.from_numpy(rows).cuda()][:, torch.from_numpy(cols).cuda()])
-    assert rel_fro(got, ref) < FRO_TOL, (M, N, K, rel_fro(got, ref))
+    qx, sx = oracle.fused_tq(xb, tb)
+    assert np.array_equal(xq.reshape(M, -1).cpu().numpy(), qx), ("activation codes", M, K)
+    assert np.array_equal(bf16_tensor_bits(xs).reshape(M, -1), sx), ("activation scales", M, K)
+    rows = np.arange(M) if stripes is None else np.concatenate([np.arange(r, r + 256) for r in stripes])
+    got = f16_tensor_f64(y[torch.from_numpy(rows).cuda()])
+    err, worst = product_check(got, qx[rows], sx[rows], qo, so, n_terms_for(M, K))
+    assert err < FRO_TOL and worst <= 1.0, (M, N, K, err, worst)
     return y
 
 
 @pytest.mark.parametrize("M", [1, 8])
 def test_cfg3_llama70b_decode(C, M):
     # BASELINE configs[2]: W4 K=8192 x N=57344, M = 1 and 8, online transform+quant then GEMV
-    _chain_case(C, M, 57344, 8192, 300 + M, 8, 2048)
+    _chain_case(C, M, 57344, 8192, 300 + M)
 
 
 @pytest.mark.parametrize("M", [1, 8, 32])
 def test_cfg4_qwen3_8b_small_batch(C, M):
     # BASELINE configs[3]: W4 K=4096 x N=24576, M = 1/8/32, fused_tq -> gemm_s4 (split-K)
-    _chain_case(C, M, 24576, 4096, 400 + M, 32, 4096)
+    _chain_case(C, M, 24576, 4096, 400 + M)
 
 
-@pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (4096, 57344, 8192)])
-def test_cfg5_prefill(C, M, N, K):
-    # BASELINE configs[4]: K=N=4096 at M=4096 and the Llama-70B FFN at M=4096
-    _chain_case(C, M, N, K, 500 + N, 16, 1024)
+def test_cfg5_prefill_square(C):
+    # BASELINE configs[4]: K=N=4096 at M=4096, every output
+    _chain_case(C, 4096, 4096, 4096, 500 + 4096)
+
+
+def test_cfg5_prefill_llama70b(C):
+    # BASELINE configs[4]: the Llama-70B FFN at M=4096: codes whole, the
+    # product on an interior 256-row stripe (one row tile of every column
+    # tile) and the last one
+    _chain_case(C, 4096, 57344, 8192, 500 + 57344, stripes=[256 * int(rng(5).integers(1, 15)), 4096 - 256])
 
 
 @pytest.mark.parametrize("M", [1, 8, 32])
