@@ -167,6 +167,19 @@ __device__ __forceinline__ uint4 h16_codes(uint32_t w, h2 s, h2 s16) {
     return r;
 }
 
+// An MFMA operand fragment (one 32-row block and K16 slice) is 1 KiB in LDS
+// and in the activation workspace: lane l's 16 bytes at 16 * l, read with one
+// ds_read_b128 (on gfx950 the fastest LDS read form for contiguous data:
+// ~169 B/clk per CU with 8 wavefronts reading, against ~152 for two
+// ds_read_b64 and ~127 for ds_read2st64_b64, measured).
+__device__ __forceinline__ h8 frag_read(const uint8_t* frag, int lane) {
+    return *reinterpret_cast<const h8*>(frag + 16 * lane);
+}
+// Store lane L's 16-byte operand v into fragment frag (LDS or global).
+__device__ __forceinline__ void frag_write(uint8_t* frag, int L, uint4 v) {
+    *reinterpret_cast<uint4*>(frag + 16 * L) = v;
+}
+
 // One load batch of a thread: 4 groups of its activation row and weight
 // column.  Scales: with VEC, sa[0..1] / sb[0..1] hold the 4 bf16 scales as
 // two packed pairs (one 8-byte load per row); otherwise sa[i] / sb[i] hold
@@ -291,7 +304,7 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
     load_batch(0, R0);
     load_batch(1, R1);
 
-    const int wofs = (wside ? kH16Op : 0) + (r >> 5) * 1024 + (r & 31) * 16;
+    const int wofs = (wside ? kH16Op : 0) + (r >> 5) * 1024;
     auto convert = [&](int buf, Batch& rr, int i) {
         if (i == 0) transpose(rr.c);
         uint8_t* dst = smem + buf * kH16Buf + wofs;
@@ -300,7 +313,7 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
         const uint32_t w4[4] = {rr.c[i].x, rr.c[i].y, rr.c[i].z, rr.c[i].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<uint4*>(dst + (j >> 1) * kH16Slice + (j & 1) * 512) = h16_codes(w4[j], sc, sc16);
+            frag_write(dst + (j >> 1) * kH16Slice, (r & 31) + 32 * (j & 1), h16_codes(w4[j], sc, sc16));
     };
 
     v16f acc[4][2];
@@ -317,11 +330,9 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
         for (int kk = 0; kk < 2; ++kk) {
             h8 af[4], bf[2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                af[i] = *reinterpret_cast<const h8*>(b0 + kk * kH16Slice + (rba + i) * 1024 + lane * 16);
+            for (int i = 0; i < 4; ++i) af[i] = frag_read(b0 + kk * kH16Slice + (rba + i) * 1024, lane);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                bf[j] = *reinterpret_cast<const h8*>(b0 + kH16Op + kk * kH16Slice + (rbb + j) * 1024 + lane * 16);
+            for (int j = 0; j < 2; ++j) bf[j] = frag_read(b0 + kH16Op + kk * kH16Slice + (rbb + j) * 1024, lane);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -444,11 +455,11 @@ __global__ __launch_bounds__(256) void h16_prep_a_kernel(const uint8_t* __restri
         }
         h2 sc, sc16;
         h16_scale(f, e, sc, sc16);
-        uint8_t* dst = a16 + ((size_t)rb * G + g) * 2048 + rr * 16;
-        *reinterpret_cast<uint4*>(dst + 0) = h16_codes(w.x, sc, sc16);
-        *reinterpret_cast<uint4*>(dst + 512) = h16_codes(w.y, sc, sc16);
-        *reinterpret_cast<uint4*>(dst + 1024) = h16_codes(w.z, sc, sc16);
-        *reinterpret_cast<uint4*>(dst + 1536) = h16_codes(w.w, sc, sc16);
+        uint8_t* dst = a16 + ((size_t)rb * G + g) * 2048;
+        frag_write(dst, rr, h16_codes(w.x, sc, sc16));
+        frag_write(dst, rr + 32, h16_codes(w.y, sc, sc16));
+        frag_write(dst + 1024, rr, h16_codes(w.z, sc, sc16));
+        frag_write(dst + 1024, rr + 32, h16_codes(w.w, sc, sc16));
     }
 }
 
@@ -577,7 +588,7 @@ void gemm_h16a_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
             x[i].w = h16_xchg<0x4E>(z[i].w, o.w, !own);
         }
     };
-    const int wofs = (r >> 5) * 1024 + (r & 31) * 16;
+    const int wofs = (r >> 5) * 1024;
     auto convert = [&](int buf, Batch& rr, int i) {
         if (i == 0) transpose(rr.c);
         uint8_t* dst = slotB(buf) + wofs;
@@ -586,7 +597,7 @@ void gemm_h16a_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
         const uint32_t w4[4] = {rr.c[i].x, rr.c[i].y, rr.c[i].z, rr.c[i].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<uint4*>(dst + (j >> 1) * kH16Slice + (j & 1) * 512) = h16_codes(w4[j], sc, sc16);
+            frag_write(dst + (j >> 1) * kH16Slice, (r & 31) + 32 * (j & 1), h16_codes(w4[j], sc, sc16));
     };
 
     v16f acc[4][2];
@@ -604,11 +615,9 @@ void gemm_h16a_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
         for (int kk = 0; kk < 2; ++kk) {
             h8 af[4], bf[2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                af[i] = *reinterpret_cast<const h8*>(a0 + kk * kH16Slice + (rba + i) * 1024 + lane * 16);
+            for (int i = 0; i < 4; ++i) af[i] = frag_read(a0 + kk * kH16Slice + (rba + i) * 1024, lane);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                bf[j] = *reinterpret_cast<const h8*>(b0 + kk * kH16Slice + (rbb + j) * 1024 + lane * 16);
+            for (int j = 0; j < 2; ++j) bf[j] = frag_read(b0 + kk * kH16Slice + (rbb + j) * 1024, lane);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
