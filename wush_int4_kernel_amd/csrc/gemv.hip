@@ -343,8 +343,12 @@ __global__ __launch_bounds__(GL == 1 ? 1024 : 256) void gemv_ks_kernel(const uin
                                                        const uint16_t* __restrict__ ws,
                                                        uint16_t* __restrict__ y, int N, int K,
                                                        int rows_per_wg) {
-    extern __shared__ __align__(16) float part[];           // [rows_per_wg][KS][M]
+    // [rows_per_wg][KS * M + 1]: the pad word puts consecutive rows of one
+    // output index in different banks for the summing loop below (without it
+    // their stride was KS * M = 32 words, one bank for a whole half-wavefront)
+    extern __shared__ __align__(16) float part[];
     const int KS = blockDim.x >> 6;
+    const int RP = KS * M + 1;                       // words per row of the partial table
     const int G = K >> 5;
     const int K2 = K >> 1;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -424,7 +428,7 @@ __global__ __launch_bounds__(GL == 1 ? 1024 : 256) void gemv_ks_kernel(const uin
                 }
                 load(i + kKsRing, d);
                 const float total = wave_reduce_scatter<V>(v, lane);
-                if (holder && i < cnt) part[(i * KS + wave) * M + idx] = total;
+                if (holder && i < cnt) part[i * RP + wave * M + idx] = total;
             }
         }
     } else {
@@ -450,15 +454,15 @@ __global__ __launch_bounds__(GL == 1 ? 1024 : 256) void gemv_ks_kernel(const uin
                     v[m] = __builtin_fmaf((float)dot32_s4(wv, xa[t][m]), sx[t][m] * sw, v[m]);
             }
             const float total = wave_reduce_scatter<V>(v, lane);
-            if (holder) part[(i * KS + wave) * M + idx] = total;
+            if (holder) part[i * RP + wave * M + idx] = total;
         }
     }
     __syncthreads();
     // outputs of the range: add the KS partials in wavefront order
     for (int o = threadIdx.x; o < M * cnt; o += blockDim.x) {
         const int m = o / cnt, i = o - m * cnt;
-        float acc = part[(i * KS) * M + m];
-        for (int q = 1; q < KS; ++q) acc += part[(i * KS + q) * M + m];
+        float acc = part[i * RP + m];
+        for (int q = 1; q < KS; ++q) acc += part[i * RP + q * M + m];
         y[(size_t)m * N + n_begin + i] = f32_to_f16_bits(acc);
     }
 }
@@ -544,9 +548,9 @@ static void launch_gemv_ks(const GemvDeviceInfo& info, const uint8_t* xq, const 
     const int KS = K / (2048 * kKsGl);
     const int per_cu = max(1, info.ks_waves_per_cu[M - 1] / KS);
     int rows = max(1, (N + per_cu * info.cus - 1) / (per_cu * info.cus));
-    while ((size_t)rows * KS * M * sizeof(float) > kGemvKsLds) rows = (rows + 1) / 2;
+    while ((size_t)rows * (KS * M + 1) * sizeof(float) > kGemvKsLds) rows = (rows + 1) / 2;
     const int blocks = (N + rows - 1) / rows;
-    gemv_ks_kernel<M, kKsGl><<<dim3(blocks), dim3(64 * KS), (size_t)rows * KS * M * sizeof(float), stream>>>(
+    gemv_ks_kernel<M, kKsGl><<<dim3(blocks), dim3(64 * KS), (size_t)rows * (KS * M + 1) * sizeof(float), stream>>>(
         xq, xs, wq, ws, y, N, K, rows);
 }
 
