@@ -25,8 +25,9 @@ How each function is pinned (closed forms, the reference tests' known answers,
 an exact-rational fp32 emulation, brute force) is listed in
 ``tests/test_oracle_pinning.py``; ``oracle_transform`` / ``fused_tq`` are
 pinned by permutation / diagonal / identity transforms, the GEMM pieces by
-brute-force integer products.  ``wush_t_solve`` (the WUSH transform
-construction, an un-vendored third-party module in the reference) is parity
+brute-force integer products.  The oracle has no WUSH T solve: the
+reference builds T with an un-vendored third-party module, and the product
+side's own closed form (``wush_int4_kernel_amd.wush_transform``) is parity
 unpinned beyond the invariants in ``tests/test_transform_invariants.py``.
 """
 from __future__ import annotations

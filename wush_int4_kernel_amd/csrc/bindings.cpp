@@ -318,7 +318,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("w4a4_gemm_cutlass_dev", &w4a4_gemm_cutlass_dev,
           "W4A4 per-tensor matmul, alpha from a 1-elem fp32 device tensor", py::arg("xq"), py::arg("wq"),
           py::arg("alpha"));
-    m.def("w4a4_gemm_s4", &w4a4_gemm_s4, "W4A4 matmul on int8 MFMA + per-group scale", py::arg("xq"),
+    m.def("w4a4_gemm_s4", &w4a4_gemm_s4,
+          "W4A4 group-scaled matmul: int8 MFMA with exact int32 group dots below prefill sizes, fp16 MFMA on "
+          "code*scale operands for prefill (M >= 256)",
+          py::arg("xq"),
           py::arg("xs"), py::arg("wq"), py::arg("ws"));
     m.def("s4_atom_selftest", &s4_atom_selftest, "verify the int8 MFMA fragment layout");
     m.def("w4a4_gemv", &w4a4_gemv, "W4A4 INT4 gemv (M=1 decode path)", py::arg("xq"), py::arg("xs"),
