@@ -625,16 +625,31 @@ def test_gemm_h16_matches_oracle(capi, M, N, K):
         assert np.isfinite(y).all()
 
 
+def _abs_product(xq, xs, wq, ws):
+    """sum over k of |x[m][k] * w[n][k]| (codes times scales), in fp64."""
+    cx = np.abs(unpack_codes(xq)).astype(np.float64)
+    cw = np.abs(unpack_codes(wq)).astype(np.float64)
+    M, K = cx.shape
+    N, G = cw.shape[0], K // 32
+    d = np.einsum("mgk,ngk->mng", cx.reshape(M, G, 32), cw.reshape(N, G, 32), optimize=True)
+    sx = np.abs(bf16_bits_to_f32(xs).astype(np.float64))
+    sw = np.abs(bf16_bits_to_f32(ws).astype(np.float64))
+    return np.einsum("mng,mg,ng->mn", d, sx, sw, optimize=True)
+
+
 @pytest.mark.parametrize("M,N,K,wide", [(2048, 8192, 4096, False), (300, 33000, 512, False),
                                          (1030, 16400, 1024, False), (512, 8192, 2048, False),
                                          (512, 8192, 2048, True), (300, 33000, 512, True)])
-def test_gemm_h16_preconverted_activations_bit_identical(capi, M, N, K, wide):
+def test_gemm_h16_preconverted_activations_agree(capi, M, N, K, wide):
     # with a workspace of wush_gemm_s4_workspace_bytes, prefill plans with
-    # N >= 8192 convert the activations once into it (gemm_h16a); without
-    # that room they are converted per tile (gemm_h16w8): the same fp16
-    # operands in the same MFMA order, so the same bits.  (512, 8192, 2048)
-    # also splits K (2 slices), compared against the no-alloc entry point,
-    # whose scratch holds the partials but not the converted activations.
+    # N >= 8192 convert the activations once into it (h16_prep_a_kernel, then
+    # gemm_h16q); without that room they are converted per tile
+    # (gemm_h16w8): the same fp16 operands, every product exact in fp32,
+    # summed in another order.  So the two outputs differ by at most the two
+    # fp32 sums' rounding (2 * K * 2^-24 * sum |x * w|, generous) plus one
+    # fp16 rounding, on every sampled output.  (512, 8192, 2048) also splits
+    # K (2 slices), compared against the no-alloc entry point, whose scratch
+    # holds the partials but not the converted activations.
     import torch
     # wide: activation scales spanning 2^35 within a row, so that tiny ones
     # reach fp16's subnormal range and the per-slice shift matters
@@ -658,10 +673,19 @@ def test_gemm_h16_preconverted_activations_bit_identical(capi, M, N, K, wide):
         capi.gemm_s4(dx.data_ptr(), dxs.data_ptr(), dw.data_ptr(), dws.data_ptr(), y_t.data_ptr(), M, N, K,
                      None, 0, _stream())
     torch.cuda.synchronize()
-    assert torch.equal(y_a.view(torch.int16), y_t.view(torch.int16)), (M, N, K)
+    ya, yt = f16_tensor_f64(y_a), f16_tensor_f64(y_t)
+    assert np.isfinite(ya).all() and np.isfinite(yt).all()
     rows, cols = _sample(g, M, 24), _sample(g, N, 800)
+    a, t = ya[np.ix_(rows, cols)], yt[np.ix_(rows, cols)]
+    A = _abs_product(xq[rows], xs[rows], wq[cols], ws[cols])
+    ulp = np.spacing(np.maximum(np.abs(a), np.abs(t)).astype(np.float16)).astype(np.float64)
+    bound = ulp + 2 * K * 2.0 ** -24 * A
+    assert (np.abs(a - t) <= bound).all(), (M, N, K, float((np.abs(a - t) / bound).max()))
+    # the two orders round differently on few outputs
+    assert np.count_nonzero(ya != yt) < 0.05 * ya.size, (M, N, K, np.count_nonzero(ya != yt))
     ref = oracle.gemm_f64(xq[rows], xs[rows], wq[cols], ws[cols])
-    assert rel_fro(f16_tensor_f64(y_a)[np.ix_(rows, cols)], ref) < FRO_TOL
+    assert rel_fro(a, ref) < FRO_TOL
+    assert rel_fro(t, ref) < FRO_TOL
 
 
 def test_gemm_h16_int_exact_and_group_dots(capi):

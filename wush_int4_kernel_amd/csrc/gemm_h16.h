@@ -22,12 +22,20 @@ int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
                     hipStream_t stream);
 
 // The same product with the activations converted once into a workspace of
-// gemm_h16a_workspace_bytes(M, K, splits) bytes (a_ws, 16-byte aligned) by a first
-// kernel, then streamed into LDS; bit-identical to launch_gemm_h16.  Needs
-// 16-byte aligned scale tensors.
-size_t gemm_h16a_workspace_bytes(int64_t M, int64_t K, int splits);
+// gemm_h16a_workspace_bytes(M, N, K, splits) bytes (a_ws, 16-byte aligned) by a
+// first kernel (with every weight column's shift), then DMA'd into LDS by
+// launch_gemm_h16q.  The same fp16 operands as launch_gemm_h16, summed in
+// another K order within blocks of four groups: equal to fp32 rounding.
+// Needs 16-byte aligned scale tensors.
+size_t gemm_h16a_workspace_bytes(int64_t M, int64_t N, int64_t K, int splits);
 int launch_gemm_h16a(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                      uint16_t* y, float* partial, int M, int N, int K, int splits, int groups_per_split,
                      void* a_ws, hipStream_t stream);
+
+// The GEMM stage of launch_gemm_h16a, one wavefront per SIMD (gemm_h16q.hip):
+// a16 / ea / eb as h16_prep_a_kernel leaves them; arguments checked there.
+int launch_gemm_h16q(const uint8_t* a16, const int* ea, const int* eb, const uint8_t* wq, const uint16_t* ws,
+                     uint16_t* y, float* partial, int M, int N, int K, int groups_per_split, int splits,
+                     hipStream_t stream);
 
 }  // namespace wush

@@ -1,0 +1,341 @@
+// gemm_h16q.hip -- the pre-converted-activation fp16-MFMA prefill GEMM with
+// one wavefront per SIMD (csrc/gemm_s4.cu:85-379 is the reference contract;
+// operands and numerics as in gemm_h16.hip).
+//
+// Workgroup: 4 wavefronts side by side, a 256 x 256 output tile, wavefront w
+// owning all 256 rows and weight columns 64w .. 64w + 63 (8 x 2 accumulator
+// blocks, 256 fp32 accumulators in AGPRs).  Because no other wavefront needs
+// its columns, a wavefront converts its weight codes straight into MFMA
+// B-operand registers: no LDS traffic for converted weights, no transpose.
+// The activations, converted once beforehand in the matching layout
+// (h16_prep_a_kernel<true>), are DMA'd into a 4-slot LDS ring four stages
+// ahead and read by all four wavefronts.
+//
+// With one wavefront per SIMD there is no second wavefront to run the memory
+// work beside the MFMAs, so every wavefront runs a software pipeline of its
+// own, issued between its 32 MFMAs of stage t: stage t+1's activation
+// fragments, the conversion of stage t+1's weights, the DMAs of stage t+4.
+// One barrier per stage.
+//
+// Every global load of the kernel is an LDS DMA issued by an asm statement
+// (activations, weight codes and scales, shifts), and the kernel orders them
+// itself: at the end of stage t a wavefront waits until its DMAs of stage
+// t+2 (and so everything it issued before them) have landed, then the barrier
+// publishes them.  Left to the compiler, LDS DMA is tracked per LDS object in
+// a small table; once the table overflows, every LDS read waits for all DMAs
+// in flight, and register loads mixed with such DMAs get waits counted
+// without them.
+//
+// Outputs: fp16 through LDS (the ring is free after the last stage), so that
+// the global stores are 16-byte row chunks instead of one 2-byte store per
+// accumulator.
+//
+// Stage layout (h16_prep_a_kernel<true>): in each block of 4 groups a lane of
+// half h reads the 32 contiguous code bytes [32h, 32h + 32) of its column
+// (groups 2h and 2h + 1); stage s of the block takes dwords 2s and 2s + 1 of
+// them (K16 slices 0 and 1).
+#include "gemm_h16_device.h"
+#include "gemm_h16.h"
+#include "setup.h"
+
+namespace wush {
+namespace {
+
+#ifndef WUSH_H16Q_SCHED
+#define WUSH_H16Q_SCHED 1                        // explicit MFMA / LDS / VALU interleave
+#endif
+
+// LDS address (wave-uniform) of a __shared__ pointer
+__device__ __forceinline__ uint32_t lds_addr(const void* l) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)l;
+}
+// 16 (4) bytes per lane from g into LDS at lds + 16 (4) * lane
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(g), "s"(lds) : "m0");
+}
+
+// Tile id -> (row tile, column tile): workgroup i runs on XCD i % 8.  Each
+// XCD walks its column tiles in groups of 8, all row tiles of a group before
+// the next, so the workgroups in flight on an XCD share 8 weight column
+// tiles and a few activation row tiles in its L2.
+__device__ __forceinline__ void h16q_tile(uint32_t id, uint32_t NC, uint32_t NR, int& tm, int& tn) {
+    if ((NC & 7) != 0) {
+        tm = (int)(id / NC);
+        tn = (int)(id % NC);
+        return;
+    }
+    constexpr uint32_t kGroup = 8;
+    const uint32_t q = id >> 3, x = id & 7;
+    const uint32_t gsize = kGroup * NR;
+    const uint32_t g = q / gsize, w = q % gsize;
+    const uint32_t width = min(kGroup, (NC >> 3) - g * kGroup);
+    tm = (int)(w / width);
+    tn = (int)((g * kGroup + w % width) * 8 + x);
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ ea, const int* __restrict__ eb,
+                      const uint8_t* __restrict__ wq, const uint16_t* __restrict__ ws, uint16_t* __restrict__ y,
+                      float* __restrict__ partial, int M, int N, int K, int groups_per_split, int splits) {
+    // activation ring (4 stages) and, per wavefront, two weight batches of 4
+    // stages: codes [4 loads][64 lanes][16 B], scales [2 columns][64 lanes][4 B]
+    __shared__ __align__(16) uint8_t sA[4][kH16Op];
+    __shared__ __align__(16) uint8_t sBc[2][4][4096];
+    __shared__ __align__(16) uint32_t sBs[2][4][128];
+    __shared__ __align__(16) int sh_e[512];      // [0, 256) rows, [256, 512) columns
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int half = lane >> 5;
+    const int l32 = lane & 31;
+    const int GR = K >> 5;
+    const int K2 = K >> 1;
+    const int limn = N - 1;
+    const int NC = (N + kH16Tile - 1) / kH16Tile;
+    const int NR = (M + kH16Tile - 1) / kH16Tile;
+    const int mpad = NR * kH16Tile, npad = NC * kH16Tile;
+    const int per_slice = NC * NR;
+
+    const int id = blockIdx.x;
+    const int slice = id / per_slice;
+    int tm, tn;
+    h16q_tile((uint32_t)(id - slice * per_slice), (uint32_t)NC, (uint32_t)NR, tm, tn);
+    const int m0 = tm * kH16Tile;
+    const int n0 = tn * kH16Tile;
+    const int gb = slice * groups_per_split;
+    const int G = min(GR - gb, groups_per_split);
+
+    // activation DMA of this wavefront: row blocks 2w, 2w + 1, both K16 slices
+    const uint8_t* asrc = a16 + ((size_t)((m0 >> 5) + 2 * wave) * GR + gb) * 2048 + lane * 16;
+    const size_t arb = (size_t)GR * 2048;
+    auto issue_a = [&](int st, int slot) {
+        const uint8_t* src = asrc + (size_t)min(st, G - 1) * 2048;   // past the slice: the last stage
+        const uint32_t dst = lds_addr(sA[slot]) + 2 * wave * 1024;
+        dma16(src, dst);
+        dma16(src + 1024, dst + kH16Slice);
+        dma16(src + arb, dst + 1024);
+        dma16(src + arb + 1024, dst + kH16Slice + 1024);
+    };
+    // this lane's two weight columns (blocks 2w and 2w + 1) and code half
+    const int colA = min(n0 + wave * 64 + l32, limn);
+    const int colB = min(n0 + wave * 64 + 32 + l32, limn);
+    const uint8_t* qa = wq + (size_t)colA * K2 + gb * 16 + half * 32;
+    const uint8_t* qb = wq + (size_t)colB * K2 + gb * 16 + half * 32;
+    const uint16_t* sa = ws + (size_t)colA * GR + gb + 2 * half;
+    const uint16_t* sb = ws + (size_t)colB * GR + gb + 2 * half;
+    constexpr int kB = 6;                        // DMAs of one weight batch
+    auto issue_b = [&](int b, int buf) {
+        const int o = min(b * kH16Batch, G - kH16Batch);
+        const uint32_t c = lds_addr(sBc[buf][wave]);
+        dma16(qa + o * 16, c);
+        dma16(qa + o * 16 + 16, c + 1024);
+        dma16(qb + o * 16, c + 2048);
+        dma16(qb + o * 16 + 16, c + 3072);
+        const uint32_t s = lds_addr(sBs[buf][wave]);
+        dma4(sa + o, s);
+        dma4(sb + o, s + 256);
+    };
+
+    v16f acc[8][2];
+    h8 fa[2][2][8];                              // [register set][K16 slice][row block]
+    h8 fb[2][2][2];                              // [register set][K16 slice][column block]
+    auto read_frag = [&](int slot, int P, int kk, int i) {
+        fa[P][kk][i] = frag_read(sA[slot] + kk * kH16Slice + i * 1024, lane);
+    };
+    int eA = 0, eB = 0;
+    // weights of stage s of batch buffer buf, column block jb: read (codes
+    // and scale), then convert into register set P
+    struct Raw {
+        uint2 w;
+        uint32_t s;
+    };
+    auto read_b = [&](int buf, int s, int jb) {
+        Raw r;
+        r.w = *reinterpret_cast<const uint2*>(sBc[buf][wave] + (2 * jb + (s >> 1)) * 1024 + lane * 16 + (s & 1) * 8);
+        r.s = sBs[buf][wave][64 * jb + lane];
+        return r;
+    };
+    auto convert_b = [&](int P, const Raw& r, int s, int jb) {
+        const float f = __uint_as_float((s & 2) ? (r.s & 0xffff0000u) : (r.s << 16));
+        h2 sc, sc16;
+        h16_scale(f, jb ? eB : eA, sc, sc16);
+        fb[P][0][jb] = __builtin_bit_cast(h8, h16_codes(r.w.x, sc, sc16));
+        fb[P][1][jb] = __builtin_bit_cast(h8, h16_codes(r.w.y, sc, sc16));
+    };
+
+    // Prologue: shifts, activation stages 0-3, weight batches 0 and 1.
+    dma4(ea + (size_t)slice * mpad + m0 + wave * 64 + lane, lds_addr(sh_e + wave * 64));   // padded rows included
+    dma4(eb + (size_t)slice * npad + n0 + wave * 64 + lane, lds_addr(sh_e + 256 + wave * 64));
+    issue_a(0, 0);
+    issue_a(1, 1);
+    issue_a(2, 2);
+    issue_a(3, 3);
+    issue_b(0, 0);
+    issue_b(1, 1);
+    WUSH_WAIT_VMCNT(kB);                         // all but batch 1
+    WUSH_LDS_BARRIER();
+    eA = sh_e[256 + wave * 64 + l32];
+    eB = sh_e[256 + wave * 64 + 32 + l32];
+    convert_b(0, read_b(0, 0, 0), 0, 0);
+    convert_b(0, read_b(0, 0, 1), 0, 1);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) read_frag(0, 0, kk, i);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16f){0.0f};
+    __builtin_amdgcn_sched_barrier(0);
+
+    for (int s0 = 0; s0 < G; s0 += 2 * kH16Batch) {
+#pragma unroll
+        for (int j = 0; j < 2 * kH16Batch; ++j) {
+            const int t = s0 + j;
+            const int P = j & 1;
+            issue_a(t + 4, j & 3);               // into the slot stage t left
+            // a batch buffer's next batch once its last stage is converted
+            if (j == 3) issue_b(s0 / kH16Batch + 2, 0);
+            if (j == 7) issue_b(s0 / kH16Batch + 3, 1);
+            // stage t + 1's weights: batch (t + 1) / 4 (buffer ((t + 1) / 4) & 1), stage (j + 1) % 4
+            const int bc = (j < 3 || j == 7) ? 0 : 1;
+            const int sc = (j + 1) & 3;
+            // its codes and scales first, ahead of the fragment reads (LDS
+            // returns in order: read late, the conversion would wait for all)
+            const Raw rw0 = read_b(bc, sc, 0), rw1 = read_b(bc, sc, 1);
+            // 32 MFMAs of stage t; between them stage t+1's 16 activation
+            // fragment reads (past the last stage they read a stale slot,
+            // unused) and its weight conversions
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+#pragma unroll
+                    for (int jb = 0; jb < 2; ++jb) {
+                        acc[i][jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[P][kk][i], fb[P][kk][jb],
+                                                                            acc[i][jb], 0, 0, 0);
+                        const int m = kk * 16 + i * 2 + jb;   // MFMA index in the stage
+                        if (m < 16) read_frag((j + 1) & 3, P ^ 1, m >> 3, m & 7);
+                        if (m == 16) convert_b(P ^ 1, rw0, sc, 0);
+                        if (m == 24) convert_b(P ^ 1, rw1, sc, 1);
+                    }
+                }
+            }
+#if WUSH_H16Q_SCHED
+            // the weight reads, then per MFMA one activation fragment read
+            // over the first 16; the conversion VALU spread over all
+#pragma unroll
+            for (int m = 0; m < 32; ++m) {
+                if (m == 0) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS read: weights
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                if (m < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read: activations
+                if (m < 16) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
+                else __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            }
+#endif
+            // activation stage t + 2 landed: the DMAs issued after its 4 are
+            // stage t+3's and t+4's (8) plus the batches of stages t-2 .. t
+            // (issued after their stage's activations); at the first stages
+            // the count also covers the prologue's DMAs
+            const int nb = (j == 3 || j == 7) + (j == 4 || j == 0) + (j == 5 || j == 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (nb == 0) WUSH_WAIT_VMCNT(8);
+            else WUSH_WAIT_VMCNT(8 + kB);
+            WUSH_LDS_BARRIER();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // The stages past the slice DMA'd copies of its last stage into the ring
+    WUSH_WAIT_VMCNT(0);
+    __syncthreads();                             // the ring is free
+
+    const int ecA = sh_e[256 + wave * 64 + l32];
+    const int ecB = sh_e[256 + wave * 64 + 32 + l32];
+    auto out_value = [&](int i, int jb, int q, int e_row) {
+        const int e_col = jb ? ecB : ecA;
+        float v = __builtin_ldexpf(acc[i][jb][q], -(e_row + e_col));
+        if (e_row == kH16NonFinite || e_col == kH16NonFinite) v = __builtin_nanf("");
+        return v;
+    };
+    if (partial != nullptr) {
+        // fp32 partials of a K slice: one store per accumulator
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) {
+            const int col = n0 + wave * 64 + jb * 32 + l32;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int rl = i * 32 + 8 * (q >> 2) + 4 * half + (q & 3);
+                    const int row = m0 + rl;
+                    const float v = out_value(i, jb, q, sh_e[rl]);
+                    if (row < M && col < N) partial[((size_t)slice * M + row) * N + col] = v;
+                }
+        }
+        return;
+    }
+    // fp16: each wavefront's 256 x 64 outputs through its ring slot (16 KiB),
+    // 128 rows at a time: 2-byte LDS writes in the accumulator layout, then
+    // 16-byte reads and stores of 8 columns of a row
+    const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+    uint8_t* stg = sA[wave];
+    uint8_t* wbase = stg + 4 * half * 128 + l32 * 2;                 // row 4 * half, column l32
+    const uint8_t* rbase = stg + (lane >> 3) * 128 + (lane & 7) * 16;
+    const int* erow = sh_e + 4 * half;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+            const int i = 4 * pass + i4;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int4 er4 = *reinterpret_cast<const int4*>(erow + 32 * i + 8 * q4);
+                const int e_r[4] = {er4.x, er4.y, er4.z, er4.w};
+#pragma unroll
+                for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const uint16_t h = f32_to_f16_bits(out_value(i, jb, 4 * q4 + r, e_r[r]));
+                        *reinterpret_cast<uint16_t*>(wbase + (32 * i4 + 8 * q4 + r) * 128 + 64 * jb) = h;
+                    }
+            }
+            __builtin_amdgcn_sched_barrier(0);   // one row block at a time
+        }
+        const int row0 = m0 + 128 * pass + (lane >> 3);
+        const int col = n0 + wave * 64 + (lane & 7) * 8;
+        uint16_t* dst0 = y + (size_t)row0 * N + col;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const uint4 v = *reinterpret_cast<const uint4*>(rbase + k * 1024);
+            if (row0 + 8 * k < M) {
+                uint16_t* dst = dst0 + (size_t)(8 * k) * N;
+                if (vec && col + 8 <= N) {
+                    *reinterpret_cast<uint4*>(dst) = v;
+                } else {
+                    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (col + e < N) dst[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+}  // namespace
+
+int launch_gemm_h16q(const uint8_t* a16, const int* ea, const int* eb, const uint8_t* wq, const uint16_t* ws,
+                     uint16_t* y, float* partial, int M, int N, int K, int groups_per_split, int splits,
+                     hipStream_t stream) {
+    const long long tiles = (long long)((N + kH16Tile - 1) / kH16Tile) * ((M + kH16Tile - 1) / kH16Tile) * splits;
+    gemm_h16q_kernel<<<dim3((unsigned)tiles), 256, 0, stream>>>(a16, ea, eb, wq, ws, y, partial, M, N, K,
+                                                                 groups_per_split, splits);
+    return (int)hipGetLastError();
+}
+
+}  // namespace wush

@@ -641,7 +641,7 @@ struct Plan {
     int splits;
     int groups_per_split;
     int tm, tn, sg;
-    bool a16 = false;  // cfg 5: activations pre-converted into the workspace (gemm_h16a)
+    bool a16 = false;  // cfg 5: activations pre-converted into the workspace (gemm_h16q.hip)
 };
 
 // Workspace layout: fp32 split-K partials [splits][M][N] from offset 0, then
@@ -653,7 +653,7 @@ static size_t plan_a16_offset(const Plan& p, int64_t M, int64_t N) {
     return (plan_partial_bytes(p, M, N) + 255) / 256 * 256;
 }
 static size_t plan_bytes(const Plan& p, int64_t M, int64_t N, int64_t K) {
-    return p.a16 ? plan_a16_offset(p, M, N) + gemm_h16a_workspace_bytes(M, K, p.splits) : plan_partial_bytes(p, M, N);
+    return p.a16 ? plan_a16_offset(p, M, N) + gemm_h16a_workspace_bytes(M, N, K, p.splits) : plan_partial_bytes(p, M, N);
 }
 
 #ifndef WUSH_PF_BM
@@ -708,7 +708,7 @@ static size_t plan_bytes(const Plan& p, int64_t M, int64_t N, int64_t K) {
 #ifndef WUSH_H16_SPLIT_MIN_M
 #define WUSH_H16_SPLIT_MIN_M 512
 #endif
-// Pre-converted activations (gemm_h16a) when the weights have at least this
+// Pre-converted activations (gemm_h16q.hip) when the weights have at least this
 // many columns, the scales are 16-byte aligned and the workspace has room
 // for M x K x 2 bytes more.
 #ifndef WUSH_H16A_MIN_N
