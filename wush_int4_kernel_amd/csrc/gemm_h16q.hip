@@ -15,7 +15,9 @@
 // work beside the MFMAs, so every wavefront runs a software pipeline of its
 // own, issued between its 32 MFMAs of stage t: stage t+1's activation
 // fragments, the conversion of stage t+1's weights, the DMAs of stage t+4.
-// One barrier per stage.
+// One barrier per stage.  A wavefront's weight codes come in batches of four
+// stages, DMA'd into LDS two batches ahead and read into registers once per
+// batch (6 LDS reads per 4 stages, not 4 per stage: 4% faster at L70).
 //
 // Every global load of the kernel is an LDS DMA issued by an asm statement
 // (activations, weight codes and scales, shifts), and the kernel orders them
@@ -147,25 +149,32 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
         fa[P][kk][i] = frag_read(sA[slot] + kk * kH16Slice + i * 1024, lane);
     };
     int eA = 0, eB = 0;
-    // weights of stage s of batch buffer buf, column block jb: read (codes
-    // and scale), then convert into register set P
-    struct Raw {
-        uint2 w;
-        uint32_t s;
+    // A weight batch in registers, read from its LDS buffer once: this
+    // lane's 32 code bytes of each of its two columns, and their scales
+    // (two bf16 per column: groups 2h and 2h + 1 of the batch's block).
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    struct Batch {
+        u32x4 c[2][2];                           // [column block][16-byte half]
+        uint32_t s[2];
     };
-    auto read_b = [&](int buf, int s, int jb) {
-        Raw r;
-        r.w = *reinterpret_cast<const uint2*>(sBc[buf][wave] + (2 * jb + (s >> 1)) * 1024 + lane * 16 + (s & 1) * 8);
-        r.s = sBs[buf][wave][64 * jb + lane];
-        return r;
+    auto read_batch = [&](int buf, Batch& r) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            r.c[k >> 1][k & 1] = *reinterpret_cast<const u32x4*>(sBc[buf][wave] + k * 1024 + lane * 16);
+        r.s[0] = sBs[buf][wave][lane];
+        r.s[1] = sBs[buf][wave][64 + lane];
     };
-    auto convert_b = [&](int P, const Raw& r, int s, int jb) {
-        const float f = __uint_as_float((s & 2) ? (r.s & 0xffff0000u) : (r.s << 16));
+    // stage s (0-3) of a batch, column block jb -> B operands of register set P
+    auto convert_b = [&](int P, const Batch& r, int s, int jb) {
+        const uint32_t sv = r.s[jb];
+        const float f = __uint_as_float((s & 2) ? (sv & 0xffff0000u) : (sv << 16));
         h2 sc, sc16;
         h16_scale(f, jb ? eB : eA, sc, sc16);
-        fb[P][0][jb] = __builtin_bit_cast(h8, h16_codes(r.w.x, sc, sc16));
-        fb[P][1][jb] = __builtin_bit_cast(h8, h16_codes(r.w.y, sc, sc16));
+        const u32x4& c = r.c[jb][s >> 1];
+        fb[P][0][jb] = __builtin_bit_cast(h8, h16_codes((s & 1) ? c[2] : c[0], sc, sc16));
+        fb[P][1][jb] = __builtin_bit_cast(h8, h16_codes((s & 1) ? c[3] : c[1], sc, sc16));
     };
+    Batch R0, R1;                                // batches in LDS buffers 0 and 1
 
     // Prologue: shifts, activation stages 0-3, weight batches 0 and 1.
     dma4(ea + (size_t)slice * mpad + m0 + wave * 64 + lane, lds_addr(sh_e + wave * 64));   // padded rows included
@@ -180,8 +189,9 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
     WUSH_LDS_BARRIER();
     eA = sh_e[256 + wave * 64 + l32];
     eB = sh_e[256 + wave * 64 + 32 + l32];
-    convert_b(0, read_b(0, 0, 0), 0, 0);
-    convert_b(0, read_b(0, 0, 1), 0, 1);
+    read_batch(0, R0);
+    convert_b(0, R0, 0, 0);
+    convert_b(0, R0, 0, 1);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -201,12 +211,15 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
             // a batch buffer's next batch once its last stage is converted
             if (j == 3) issue_b(s0 / kH16Batch + 2, 0);
             if (j == 7) issue_b(s0 / kH16Batch + 3, 1);
-            // stage t + 1's weights: batch (t + 1) / 4 (buffer ((t + 1) / 4) & 1), stage (j + 1) % 4
-            const int bc = (j < 3 || j == 7) ? 0 : 1;
+            // stage t + 1's weights: batch (t + 1) / 4, in LDS buffer
+            // ((t + 1) / 4) & 1, stage (j + 1) % 4 of it.  A batch goes into
+            // registers at the stage before its first, ahead of that stage's
+            // fragment reads (LDS returns in order: read late, the
+            // conversion would wait for all of them).
+            if (j == 3) read_batch(1, R1);
+            if (j == 7) read_batch(0, R0);
+            const Batch& Rc = (j < 3 || j == 7) ? R0 : R1;
             const int sc = (j + 1) & 3;
-            // its codes and scales first, ahead of the fragment reads (LDS
-            // returns in order: read late, the conversion would wait for all)
-            const Raw rw0 = read_b(bc, sc, 0), rw1 = read_b(bc, sc, 1);
             // 32 MFMAs of stage t; between them stage t+1's 16 activation
             // fragment reads (past the last stage they read a stale slot,
             // unused) and its weight conversions
@@ -220,17 +233,17 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
                                                                             acc[i][jb], 0, 0, 0);
                         const int m = kk * 16 + i * 2 + jb;   // MFMA index in the stage
                         if (m < 16) read_frag((j + 1) & 3, P ^ 1, m >> 3, m & 7);
-                        if (m == 16) convert_b(P ^ 1, rw0, sc, 0);
-                        if (m == 24) convert_b(P ^ 1, rw1, sc, 1);
+                        if (m == 16) convert_b(P ^ 1, Rc, sc, 0);
+                        if (m == 24) convert_b(P ^ 1, Rc, sc, 1);
                     }
                 }
             }
 #if WUSH_H16Q_SCHED
-            // the weight reads, then per MFMA one activation fragment read
-            // over the first 16; the conversion VALU spread over all
+            // a batch's reads, then per MFMA one activation fragment read over
+            // the first 16; the conversion VALU spread over all
 #pragma unroll
             for (int m = 0; m < 32; ++m) {
-                if (m == 0) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS read: weights
+                if (m == 0 && (j == 3 || j == 7)) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);   // DS read: batch
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                 if (m < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read: activations
                 if (m < 16) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
