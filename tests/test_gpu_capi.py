@@ -745,10 +745,11 @@ def test_gemm_h16_group_scale_boundary(capi):
     # One activation group at 2^-k of its row's largest scale (full 8-bit
     # significands; the largest sits in group 0, whose codes are 0), one weight
     # group nonzero.  The shifted largest scale lies in [2^12, 2^13), so the
-    # fp16 operand s/16 of the tested group keeps all 8 bits down to k = 25:
-    # y = fp16(sx * sw * D) exactly.  Below, s/16 rounds to fp16's subnormal
-    # spacing: each product term is off by at most 2^-27 * sx_max * sw_max,
-    # on top of the fp32 sum of 32 terms and the fp16 rounding of y.
+    # fp16 scale operand of the tested group keeps all 8 bits (lowest bit at
+    # or above 2^-24) down to k = 29: y = fp16(sx * sw * D) exactly.  Below,
+    # it rounds to fp16's subnormal spacing: each product term is off by at
+    # most 2^-31 * sx_max * sw_max (2^-27 taken: generous), on top of the fp32
+    # sum of 32 terms and the fp16 rounding of y.
     g = rng(4516)
     M, N, K = 512, 32768, 256
     G = K // 32
@@ -761,7 +762,7 @@ def test_gemm_h16_group_scale_boundary(capi):
     A = oracle.group_dots(pack_codes(np.abs(unpack_codes(xq[rows]))),
                           pack_codes(np.abs(unpack_codes(wq[cols])))).astype(np.float64)
     top = (((127 + g.integers(-2, 1, M)) << 7) | g.integers(0, 128, M)).astype(np.uint16)   # [0.25, 2)
-    for k in (22, 25, 26, 28, 33):
+    for k in (22, 25, 26, 29, 30, 33):
         gg = 1 + k % (G - 1)
         xs = np.zeros((M, G), np.uint16)
         ws = np.zeros((N, G), np.uint16)
@@ -772,7 +773,7 @@ def test_gemm_h16_group_scale_boundary(capi):
         sx = bf16_bits_to_f32(xs[rows, gg]).astype(np.float64)
         sw = bf16_bits_to_f32(ws[cols, gg]).astype(np.float64)
         exact = sx[:, None] * sw[None, :] * D[:, :, gg]
-        if k <= 25:
+        if k <= 29:
             assert np.array_equal(y, exact.astype(np.float16).astype(np.float64)), k
         else:
             sx_max = bf16_bits_to_f32(top[rows]).astype(np.float64)

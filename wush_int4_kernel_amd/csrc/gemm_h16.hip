@@ -16,9 +16,9 @@
 // row's largest scale so that it lands in [2^12, 2^13) (code * scale <= 7 *
 // 2^13 < 65504); likewise 2^eb[n] per weight column.  The epilogue multiplies
 // by 2^-(ea[m] + eb[n]) with v_ldexp_f32 (exact).  Every scale down to
-// 2^-22 of its row's largest converts exactly; smaller ones land in fp16's
-// subnormal range and keep fewer bits (an absolute error below 2^-36 of the
-// row's largest scale per term).  A row or column with a non-finite scale
+// 2^-29 of its row's largest converts exactly (its lowest significand bit
+// stays at or above fp16's 2^-24); smaller ones keep fewer bits (an absolute
+// error below 2^-37 of the row's largest scale per scale operand).  A row or column with a non-finite scale
 // gives NaN, as the reference's dequantized product does (code 0 * inf).
 //
 // Workgroup: 8 wavefronts in 2 x 4, a 256 x 256 output tile, each wavefront
@@ -152,12 +152,11 @@ void gemm_h16w8_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restric
     auto convert = [&](int buf, Batch& rr, int i) {
         if (i == 0) transpose(rr.c);
         uint8_t* dst = smem + buf * kH16Buf + wofs;
-        h2 sc, sc16;
-        h16_scale(h16_batch_scale<VEC>(rr.s, i), e, sc, sc16);
+        const h2 sc = h16_scale(h16_batch_scale<VEC>(rr.s, i), e);
         const uint32_t w4[4] = {rr.c[i].x, rr.c[i].y, rr.c[i].z, rr.c[i].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            frag_write(dst + (j >> 1) * kH16Slice, (r & 31) + 32 * (j & 1), h16_codes(w4[j], sc, sc16));
+            frag_write(dst + (j >> 1) * kH16Slice, (r & 31) + 32 * (j & 1), h16_codes(w4[j], sc));
     };
 
     v16f acc[4][2];
@@ -315,16 +314,15 @@ __global__ __launch_bounds__(256) void h16_prep_a_kernel(const uint8_t* __restri
             w = *reinterpret_cast<const uint4*>(xq + (size_t)row * (K >> 1) + g * 16);
             f = __uint_as_float((uint32_t)xs[(size_t)row * G + g] << 16);
         }
-        h2 sc, sc16;
-        h16_scale(f, e, sc, sc16);
+        const h2 sc = h16_scale(f, e);
         const int q = g & 3;
         const int st = (g & ~3) + 2 * (q & 1);                // stage of dwords 0, 1 (2, 3: st + 1)
         uint8_t* dst = a16 + ((size_t)rb * G + st) * 2048;
         const int L = rr + 32 * (q >> 1);
-        frag_write(dst, L, h16_codes(w.x, sc, sc16));
-        frag_write(dst + 1024, L, h16_codes(w.y, sc, sc16));
-        frag_write(dst + 2048, L, h16_codes(w.z, sc, sc16));
-        frag_write(dst + 3072, L, h16_codes(w.w, sc, sc16));
+        frag_write(dst, L, h16_codes(w.x, sc));
+        frag_write(dst + 1024, L, h16_codes(w.y, sc));
+        frag_write(dst + 2048, L, h16_codes(w.z, sc));
+        frag_write(dst + 3072, L, h16_codes(w.w, sc));
     }
 }
 

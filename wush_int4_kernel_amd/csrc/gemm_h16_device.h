@@ -91,45 +91,43 @@ __device__ __forceinline__ void h16_row_max(const uint16_t* __restrict__ pa, con
     mxb = max((uint32_t)mb.x, (uint32_t)mb.y);
 }
 
-// Scale operand pair (s, s) and (s/16, s/16) in fp16 for the fp32 value f
-// of a bf16 scale and the row's shift.
-__device__ __forceinline__ void h16_scale(float f, int shift, h2& s, h2& s16) {
+// Scale operand pair (s, s) in fp16 for the fp32 value f of a bf16 scale
+// and the row's shift.
+__device__ __forceinline__ h2 h16_scale(float f, int shift) {
     const _Float16 a = (_Float16)__builtin_ldexpf(f, shift);
-    const _Float16 c = (_Float16)__builtin_ldexpf(f, shift - 4);
-    s = (h2){a, a};
-    s16 = (h2){c, c};
+    return (h2){a, a};
 }
 
 // 8 s4 codes (element 2k in the low nibble of byte k) -> 8 fp16 code*scale
 // values, in the order k = 0,4,1,5,2,6,3,7 (the same for both operands, so
-// the dot product only sums in another order).  After the XOR each nibble is
-// code + 8 in [1, 15]; OR-ing it into 0x6400 (1024.0) gives 1024 + code + 8
-// (low nibble) or 1024 + 16 * (code + 8) (high nibble of a byte), both exact;
-// the subtraction leaves code or 16 * code exactly and the product with s or
-// s/16 is one exact fp16 rounding.
-// (a & b) | c in one v_bitop3_b32 (truth table 0xEA for src0 = a, src1 = b,
-// src2 = c); left to itself the compiler fuses the XOR below into the AND
-// instead and spends a v_or_b32 per pair.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t b, uint32_t c) {
+// the dot product only sums in another order).  One v_bitop3_b32 per pair
+// (truth table 0x6A: b ? a ^ c : c, for src0 = a, src1 = b, src2 = c) keeps
+// a nibble (b = its mask), flips its top bit (c = 1 there: two's complement
+// -> code + 8 in [0, 15]) and sets the fp16 exponent bits of the constant
+// (b = 0, c = 1).  A low nibble lands in mantissa bits 0-3 of 1024.0
+// (0x6400, ulp 1): 1024 + code + 8.  A high nibble (bits 4-7) lands in
+// mantissa bits 4-7 of 64.0 (0x5400, ulp 1/16, so bits 4-7 weigh 1..8):
+// 64 + code + 8.  Subtracting 1032 or 72 leaves the code exactly, and the
+// product with s is one exact fp16 rounding.
+__device__ __forceinline__ uint32_t h16_nib(uint32_t a, uint32_t b, uint32_t c) {
     uint32_t r;
-    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0xea" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x6a" : "=v"(r) : "v"(a), "v"(b), "v"(c));
     return r;
 }
 
-__device__ __forceinline__ uint4 h16_codes(uint32_t w, h2 s, h2 s16) {
-    const uint32_t t = w ^ 0x88888888u;
-    const uint32_t t8 = t >> 8;
+__device__ __forceinline__ uint4 h16_codes(uint32_t w, h2 s) {
+    const uint32_t w8 = w >> 8;
     const h2 b0 = {(_Float16)1032.0f, (_Float16)1032.0f};
-    const h2 b1 = {(_Float16)1152.0f, (_Float16)1152.0f};
-    const h2 p0 = __builtin_bit_cast(h2, and_or(t, 0x000F000Fu, 0x64006400u));
-    const h2 p1 = __builtin_bit_cast(h2, and_or(t, 0x00F000F0u, 0x64006400u));
-    const h2 p2 = __builtin_bit_cast(h2, and_or(t8, 0x000F000Fu, 0x64006400u));
-    const h2 p3 = __builtin_bit_cast(h2, and_or(t8, 0x00F000F0u, 0x64006400u));
+    const h2 b1 = {(_Float16)72.0f, (_Float16)72.0f};
+    const h2 p0 = __builtin_bit_cast(h2, h16_nib(w, 0x000F000Fu, 0x64086408u));
+    const h2 p1 = __builtin_bit_cast(h2, h16_nib(w, 0x00F000F0u, 0x54805480u));
+    const h2 p2 = __builtin_bit_cast(h2, h16_nib(w8, 0x000F000Fu, 0x64086408u));
+    const h2 p3 = __builtin_bit_cast(h2, h16_nib(w8, 0x00F000F0u, 0x54805480u));
     uint4 r;
     r.x = __builtin_bit_cast(uint32_t, (h2)((p0 - b0) * s));
-    r.y = __builtin_bit_cast(uint32_t, (h2)((p1 - b1) * s16));
+    r.y = __builtin_bit_cast(uint32_t, (h2)((p1 - b1) * s));
     r.z = __builtin_bit_cast(uint32_t, (h2)((p2 - b0) * s));
-    r.w = __builtin_bit_cast(uint32_t, (h2)((p3 - b1) * s16));
+    r.w = __builtin_bit_cast(uint32_t, (h2)((p3 - b1) * s));
     return r;
 }
 

@@ -168,11 +168,10 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
     auto convert_b = [&](int P, const Batch& r, int s, int jb) {
         const uint32_t sv = r.s[jb];
         const float f = __uint_as_float((s & 2) ? (sv & 0xffff0000u) : (sv << 16));
-        h2 sc, sc16;
-        h16_scale(f, jb ? eB : eA, sc, sc16);
+        const h2 sc = h16_scale(f, jb ? eB : eA);
         const u32x4& c = r.c[jb][s >> 1];
-        fb[P][0][jb] = __builtin_bit_cast(h8, h16_codes((s & 1) ? c[2] : c[0], sc, sc16));
-        fb[P][1][jb] = __builtin_bit_cast(h8, h16_codes((s & 1) ? c[3] : c[1], sc, sc16));
+        fb[P][0][jb] = __builtin_bit_cast(h8, h16_codes((s & 1) ? c[2] : c[0], sc));
+        fb[P][1][jb] = __builtin_bit_cast(h8, h16_codes((s & 1) ? c[3] : c[1], sc));
     };
     Batch R0, R1;                                // batches in LDS buffers 0 and 1
 
