@@ -833,6 +833,106 @@ def test_gemm_h16_nonfinite_scales(capi):
     assert rel_fro(got, ref) < FRO_TOL, rel_fro(got, ref)
 
 
+# Shapes the planner sends to the fp16-MFMA streaming kernel (gemm_h16s:
+# 32 < M <= 64, 224-column workgroups filling 7/8 to all of 256 CUs, i.e.
+# 49953 <= N <= 57344, K % 1024 == 0, 16-byte aligned operands): two 32-row
+# activation blocks, the second ragged; ragged N (a partial last column
+# block and workgroup); 4 to 32 batches of 8 groups.
+H16S_SHAPES = [(33, 50000, 2048), (37, 57344, 1024), (41, 52000, 1024), (48, 56000, 3072), (64, 57344, 6144),
+               (40, 57300, 8192), (57, 57344, 4096)]
+
+
+@pytest.mark.parametrize("M,N,K", H16S_SHAPES)
+def test_gemm_h16s_matches_oracle(capi, M, N, K):
+    # fp16 operands code*scale (exact), fp32 accumulation over all of K:
+    # seeded samples of columns (first and last always) against the fp64
+    # oracle, every row, within each output's own bound (fp16 rounding plus
+    # 2K rounded fp32 additions) and the 2e-3 gate
+    g = rng(4800 + M + N + K)
+    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    cols = _sample(g, N, 1500)
+    y = run_gemm(capi, xq, xs, wq, ws)
+    assert np.isfinite(y).all()
+    got = y[:, cols]
+    ref = oracle.gemm_f64(xq, xs, wq[cols], ws[cols])
+    assert rel_fro(got, ref) < FRO_TOL, (M, N, K, rel_fro(got, ref))
+    A = _abs_product(xq, xs, wq[cols], ws[cols])
+    bound = (np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) + 2 * K * 2.0 ** -24 * A
+             + 2.0 ** -25)
+    assert (np.abs(got - ref) <= bound).all(), (M, N, K, float((np.abs(got - ref) / bound).max()))
+
+
+def test_gemm_h16s_int_exact_and_group_dots(capi):
+    # unit scales and small codes: integer sums, exact; then scales 1 on one
+    # group only (both lane halves and all four positions of an 8-group
+    # batch, first and last batches): y = D[:, :, g] exactly
+    g = rng(4810)
+    M, N, K = 40, 51200, 2048
+    xq = pack_codes(g.integers(-2, 3, (M, K)))
+    wq = pack_codes(g.integers(-2, 3, (N, K)))
+    xs = np.full((M, K // 32), 0x3F80, np.uint16)
+    ws = np.full((N, K // 32), 0x3F80, np.uint16)
+    cols = _sample(g, N, 1024)
+    y = run_gemm(capi, xq, xs, wq, ws)
+    D = oracle.group_dots(xq, wq[cols]).astype(np.float64)
+    assert np.array_equal(y[:, cols], D.sum(axis=2))
+    xq, _, wq, _ = _rand_operands(g, M, N, K)
+    D = oracle.group_dots(xq, wq[cols]).astype(np.float64)
+    for gg in (0, 7, 8, 15, 16, 31, 33, 47, 56, 63):
+        xs = np.zeros((M, K // 32), np.uint16)
+        ws = np.zeros((N, K // 32), np.uint16)
+        xs[:, gg] = 0x3F80
+        ws[:, gg] = 0x3F80
+        y = run_gemm(capi, xq, xs, wq, ws)
+        assert np.array_equal(y[:, cols], D[:, :, gg]), gg
+        assert np.count_nonzero(np.delete(y, cols, axis=1) != 0) > 0
+
+
+def test_gemm_h16s_scale_range_and_quarters(capi):
+    # Scales far outside fp16's range (rows near 2^+40, columns near 2^-40),
+    # and a different order of magnitude in each K quarter of a row (2^-12,
+    # 2^0, 2^+6, 2^-6), so that a row's shift comes from one quarter and the
+    # others sit up to 2^-18 below it (still exact); the row and column
+    # factors (2^-3 .. 2^0) keep every output inside fp16's range.  Compared
+    # with the oracle after removing each row's and column's factor.
+    g = rng(4820)
+    M, N, K = 36, 50400, 4096
+    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    G = K // 32
+    dr = g.integers(-3, 1, M)
+    dc = g.integers(-3, 1, N)
+    quarter = np.repeat(np.array([-12, 0, 6, -6]), G // 4)[None, :]
+    xs2 = _bf16_times_pow2(xs, 40 + dr[:, None] + quarter)
+    ws2 = _bf16_times_pow2(ws, -40 + dc[:, None])
+    cols = _sample(g, N, 1500)
+    ref = oracle.gemm_f64(xq, _bf16_times_pow2(xs, quarter + 0 * dr[:, None]), wq[cols], ws[cols])
+    y = run_gemm(capi, xq, xs2, wq, ws2)[:, cols]
+    assert np.isfinite(y).all()
+    got = y * np.ldexp(1.0, -(dr[:, None] + dc[cols][None, :]))
+    assert rel_fro(got, ref) < FRO_TOL, rel_fro(got, ref)
+
+
+def test_gemm_h16s_nonfinite_scales(capi):
+    # a non-finite activation scale makes its row NaN, a non-finite weight
+    # scale its column (wherever in K it sits); the rest is unaffected
+    g = rng(4830)
+    M, N, K = 44, 50500, 2048
+    xq, xs, wq, ws = _rand_operands(g, M, N, K)
+    xs[3, 2] = 0x7F80                            # +inf, quarter 0
+    xs[17, 50] = 0xFFC0                          # NaN, quarter 3
+    ws[5, 20] = 0x7FC0                           # NaN, quarter 1
+    ws[8400, 40] = 0xFF80                        # -inf, quarter 2
+    y = run_gemm(capi, xq, xs, wq, ws)
+    bad_r, bad_c = [3, 17], [5, 8400]
+    assert np.isnan(y[bad_r]).all() and np.isnan(y[:, bad_c]).all()
+    rows = np.array([r for r in range(M) if r not in bad_r])
+    cols = np.array([c for c in _sample(g, N, 1500) if c not in bad_c])
+    ref = oracle.gemm_f64(xq[rows], xs[rows], wq[cols], ws[cols])
+    got = y[np.ix_(rows, cols)]
+    assert np.isfinite(got).all()
+    assert rel_fro(got, ref) < FRO_TOL, rel_fro(got, ref)
+
+
 def test_gemm_golden_fixture(capi):
     gm = np.load(os.path.join(GOLDEN, "gemm_small.npz"))
     y = run_gemm(capi, gm["xq"], gm["xs"], gm["wq"], gm["ws"])

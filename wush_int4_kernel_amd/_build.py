@@ -26,7 +26,7 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libwush_int4.so")
 EXT = os.path.join(PKG, "_C" + sysconfig.get_config_var("EXT_SUFFIX"))
 
-HIP_SOURCES = ["quant.hip", "fused_tq.hip", "gemv.hip", "gemm_s4.hip", "gemm_h16.hip", "gemm_h16q.hip", "setup.hip"]
+HIP_SOURCES = ["quant.hip", "fused_tq.hip", "gemv.hip", "gemm_s4.hip", "gemm_h16.hip", "gemm_h16q.hip", "gemm_h16s.hip", "setup.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -49,8 +49,9 @@ VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def source_flags(src: str) -> list:
-    # gemm_h16q.hip holds 256 fp32 accumulators per lane: they live in AGPRs
-    return HIPCC_FLAGS + ([] if src == "gemm_h16q.hip" else VGPR_FORM)
+    # gemm_h16q.hip and gemm_h16s.hip hold up to 256 fp32 accumulators per
+    # lane: they live in AGPRs
+    return HIPCC_FLAGS + ([] if src in ("gemm_h16q.hip", "gemm_h16s.hip") else VGPR_FORM)
 
 
 def _run(cmd, verbose):

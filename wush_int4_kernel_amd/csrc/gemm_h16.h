@@ -38,4 +38,13 @@ int launch_gemm_h16q(const uint8_t* a16, const int* ea, const int* eb, const uin
                      uint16_t* y, float* partial, int M, int N, int K, int groups_per_split, int splits,
                      hipStream_t stream);
 
+// The product for 32 < M <= 64 on weight matrices whose 224-column blocks
+// fill the GPU in one round (gemm_h16s.hip; the rule is gemm_h16s_shape_ok):
+// fp16 operands as above, the weights streamed once, no workspace.  Needs
+// K % 1024 == 0 and 16-byte aligned code and scale tensors.
+bool gemm_h16s_shape_ok(int64_t M, int64_t N, int64_t K);
+bool gemm_h16s_supported(int64_t M, int64_t N, int64_t K, const void* xs, const void* ws);
+int launch_gemm_h16s(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws, uint16_t* y,
+                     int M, int N, int K, hipStream_t stream);
+
 }  // namespace wush

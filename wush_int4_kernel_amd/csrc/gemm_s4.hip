@@ -636,7 +636,8 @@ __global__ void mfma_selftest_kernel(const int8_t* __restrict__ a, const int8_t*
 struct Plan {
     int cfg;        // 0: 32x128 (M <= 32), 1: 64x128, 2: 128x128,
                     // 4: streaming with in-workgroup K split (M <= 64),
-                    // 5: 256x256 fp16-MFMA tiles (gemm_h16.hip)
+                    // 5: 256x256 fp16-MFMA tiles (gemm_h16.hip),
+                    // 6: fp16-MFMA streaming, 8 < M <= 64 (gemm_h16s.hip)
     int mr;         // fold rows per 32-row block (cfg 0, 4)
     int splits;
     int groups_per_split;
@@ -767,13 +768,20 @@ constexpr int stream32_kw(int mr, int64_t n = 0) {
 }
 constexpr int kStream32Waves = WUSH_S32_WAVES;
 
-// scales16: both scale tensors are 16-byte aligned (the streaming kernels
-// read them 8 groups at a time).
+// scales16: both scale tensors (and both code tensors) are 16-byte aligned
+// (the streaming kernels read them 16 bytes at a time).
 static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available, bool allow_split,
                       bool scales16, bool allow_a16 = true) {
     Plan p;
     p.mr = 32;
     const int64_t G0 = K / 32;
+    if (allow_split && scales16 && gemm_h16s_shape_ok(M, N, K)) {
+        // wide weights at 8 < M <= 64: fp16-MFMA streaming, no workspace
+        p.cfg = 6; p.tm = 32; p.tn = 32; p.sg = 16;
+        p.splits = 1;
+        p.groups_per_split = (int)G0;
+        return p;
+    }
     if (allow_split && scales16 && M <= kStream32MaxM && K % 256 == 0) {
         // in-workgroup K split: one workgroup of stream32_kw wavefronts per
         // 32-row block; split K across workgroups only while fewer than
@@ -866,13 +874,17 @@ template <bool PT>
 static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                     uint16_t* y, int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes,
                     float alpha, const float* alpha_dev, hipStream_t stream, bool allow_a16 = true) {
-    const bool scales16 = ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws)) & 15u) == 0;
+    const bool scales16 = ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws) |
+                            reinterpret_cast<uintptr_t>(xq) | reinterpret_cast<uintptr_t>(wq)) & 15u) == 0;
     // the pre-converted activations need a 16-byte aligned workspace
     allow_a16 = allow_a16 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0;
     const Plan p = make_plan(M, N, K, workspace ? ws_bytes : 0, !PT, scales16, allow_a16);
     WUSH_REQUIRE((N + p.tn - 1) / p.tn <= 0x7fffffffLL && (M + p.tm - 1) / p.tm <= 65535);
     float* partial = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int m = (int)M, n = (int)N, k = (int)K;
+    if (p.cfg == 6) {
+        if constexpr (!PT) return launch_gemm_h16s(xq, xs, wq, ws, y, m, n, k, stream);
+    }
     if (p.cfg == 5) {
         if constexpr (!PT) {
             uint8_t* wsp = static_cast<uint8_t*>(workspace);
@@ -988,7 +1000,8 @@ int wush_gemm_s4_noalloc(const uint8_t* xq, const uint16_t* xs, const uint8_t* w
     // split-K partials only (no pre-converted activations), with fewer K
     // slices where the shape's full split would need more than the scratch
     // (one slice needs none, so every shape has such a plan)
-    const bool scales16 = ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws)) & 15u) == 0;
+    const bool scales16 = ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(ws) |
+                            reinterpret_cast<uintptr_t>(xq) | reinterpret_cast<uintptr_t>(wq)) & 15u) == 0;
     const size_t cap = (size_t)WUSH_GEMM_SCRATCH_BYTES;
     const size_t need = wush::plan_bytes(wush::make_plan(M, N, K, cap, true, scales16, false), M, N, K);
     if (need > cap) return WUSH_ERROR_SCRATCH_TOO_SMALL;
