@@ -117,9 +117,10 @@ size_t wush_gemm_s4_workspace_bytes(int64_t M, int64_t N, int64_t K);
  * wush_gemv_int4, y (M, N) fp16.  On int8 MFMA with exact int32 group dots,
  * except for prefill shapes (K % 256 == 0, M >= 256, at least 64 tiles of
  * 256x256 or N >= 2048, and at least 128 workgroups counting the K slices of
- * at least 32 groups each that the workspace holds from M = 512), which run
- * fp16 MFMA on code*scale operands (exact after a
- * power-of-two shift per row and column) accumulated in fp32 over all of K.
+ * at least 32 groups each that the workspace holds from M = 512) and for
+ * 32 < M <= 64 with 49953 <= N <= 57344 and K % 1024 == 0 (16-byte aligned
+ * codes and scales), which run fp16 MFMA on code*scale operands (exact after
+ * a power-of-two shift per row and column) accumulated in fp32 over all of K.
  * Both agree with the fp64 product to 2e-3 relative Frobenius (tested); a row
  * or column with a non-finite scale gives NaN there.
  * Replaces w4a4_gemm_s4 (csrc/gemm_s4.cu:320-379) and the superseded
