@@ -410,6 +410,7 @@ def main():
         launch_product("gemv", 1, N, K, wq, ws)            # L70 M=1 decode
         launch_product("gemv", 8, N, K, wq, ws)            # L70 M=8 decode
         launch_product("gemm", 32, N, K, wq, ws)           # L70 M=32 (in-workgroup K-split streaming GEMM)
+        launch_product("gemm", 64, N, K, wq, ws)           # L70 M=64 (fp16-MFMA streaming GEMM)
         for _ in range(3):
             _C.fused_transform_quant_int4_smallm(activations(1, gdev).to(torch.bfloat16), T)
             _C.fused_transform_quant_int4(activations(4096, gdev).to(torch.bfloat16), T)
