@@ -164,13 +164,6 @@ __device__ __forceinline__ float h16_batch_scale(const uint32_t (&v)[kH16Batch],
     return __uint_as_float(v[i] << 16);
 }
 
-// s_waitcnt vmcnt(n) (n < 64) with the other counters left alone, and a
-// workgroup barrier after this wavefront's LDS operations (no wait on vector
-// memory).  The LDS wait is a builtin, so that the compiler's own wait
-// insertion knows every earlier LDS operation has completed (after an asm
-// wait it still counts them outstanding and waits for later operations too).
-#define WUSH_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
-#define WUSH_LDS_BARRIER() do { __builtin_amdgcn_s_waitcnt(0xC07F); asm volatile("s_barrier" ::: "memory"); } while (0)
 
 }  // namespace
 }  // namespace wush

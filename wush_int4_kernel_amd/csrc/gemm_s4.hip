@@ -326,53 +326,63 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const uint8_t* __restrict_
 constexpr int kStreamSG = 8;                     // groups per stage
 constexpr int kStreamPlane = 32 * 8 + 16;        // bytes per (group, half) plane of a 32-row block
 
-__device__ __forceinline__ void swap_halves(uint4& v) {
-    // v_permlane32_swap(vdst, vsrc) exchanges vdst of lanes 32-63 with vsrc of
-    // lanes 0-31.  With lane l holding group g and lane l+32 group g+1 of the
-    // same row, afterwards (x,y) hold k-half (l/32) of group g and (z,w) the
-    // same k-half of group g+1.
-    auto a = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
-    auto b = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
-    v.x = a[0]; v.z = a[1];
-    v.y = b[0]; v.w = b[1];
-}
-
 // ---------------------------- streaming kernel, 8 < M <= 32, K split in-workgroup
 // One workgroup per 32-row weight block (and global K slice); its KW
-// wavefronts take the slice's stages round-robin (wavefront w: stages w,
-// w + KW, ...), so KW neighbouring 128-byte lines of every row are in flight
-// together and a Llama-70B FFN layer (N = 57344) runs 7168 wavefronts -- 7 per
-// SIMD, evenly -- where one wavefront per block gives 1792, i.e. 1 or 2 per
-// SIMD with the fold work of two on the busiest ones.  Per stage a wavefront
-// loads the block's weights (coalesced, transposed through its LDS slab), the
-// activations (whole 16-byte groups, re-paired
-// with v_permlane32_swap) and, per lane, 16 bytes of bf16 scales for its
-// activation row and its weight column.  Addresses are a wave-uniform base
-// plus a 32-bit lane offset (no 64-bit address arithmetic per load).
+// wavefronts take contiguous runs of the slice's stages (wavefront w: stages
+// [w c, (w+1) c)), so a Llama-70B FFN layer (N = 57344) runs 7168 wavefronts.
+// Every global load is whole 128-byte lines or, for scales, whole 64-byte
+// runs: a load instruction whose 64 lanes touch 32 different lines costs the
+// vector memory path about as much as one that reads them whole (measured:
+// with each row's 16- and 32-byte pieces loaded per lane, the L70 M=32 kernel
+// took 80 us; without the scale loads alone, 54).  Per stage a wavefront loads
+// the block's weights and the activations as 8 rows x 128 bytes per
+// instruction, both transposed through its LDS slab, and every fourth stage
+// the next four stages' bf16 scales of its activation rows and weight columns
+// by LDS DMA (64 contiguous bytes per row).  Addresses are a wave-uniform
+// base plus a 32-bit lane offset (no 64-bit address arithmetic per load).
 //
 // Fold factors: the bf16 MFMA takes the lane's 8 activation scales of the
-// stage as they were loaded and a weight-scale operand holding only group g's
-// scale (the other 7 elements zero), so each factor is 2*sx[g]*sw[g] exactly.
-// The four weight operands (one per scale dword) keep their zero elements in
-// registers across the loop: one AND per group builds an operand.  A
-// non-finite activation scale meets a zero and gives NaN for its whole row,
-// as the reference's dequantized product does (code 0 * inf scale).
-// Groups are software pipelined: group g+1's two MFMAs are issued before
-// group g's fold.  At the end the KW partial accumulators go through LDS and
-// are summed in wavefront order (deterministic).  Requires K % 256 == 0,
-// 16-byte aligned scales and slices of whole stages.
+// stage and a weight-scale operand holding only group g's scale (the other 7
+// elements zero), so each factor is 2*sx[g]*sw[g] exactly.  The four weight
+// operands (one per scale dword) keep their zero elements in registers across
+// the loop: one AND per group builds an operand.  A non-finite activation
+// scale meets a zero and gives NaN for its whole row, as the reference's
+// dequantized product does (code 0 * inf scale).  Groups are software
+// pipelined: group g+1's two MFMAs are issued before group g's fold.  At the
+// end the KW partial accumulators go through LDS and are summed in wavefront
+// order (deterministic).  Requires K % 256 == 0, 16-byte aligned scales and
+// slices of whole stages.
 template <int MB>
 struct Stream32Stage {
     uint4 w[4];         // weight line chunks: row 8j + lane/8, group lane%8
-    uint4 x[MB][4];     // per activation block b: groups 2t + half of row 32b + lane%32
-    uint4 sx[MB];       // 8 bf16 activation scales of that row
-    uint4 sw;           // 8 bf16 weight scales of column lane%32
+    uint4 x[MB][4];     // activation line chunks: row 32b + 8j + lane/8, group lane%8
 };
+// the bf16 scales of one stage: activation row 32b + lane%32, weight column lane%32
+template <int MB>
+struct Stream32Scales {
+    uint4 sx[MB];
+    uint4 sw;
+};
+constexpr int kStreamXRow = 2 * 64 + 16;         // slab bytes per activation row: [k-half][group][8 B] + pad
+constexpr int kStreamSC = 4;                     // stages per scale DMA
+constexpr int kStreamSBlock = 32 * kStreamSC * 16;   // slab bytes per 32-row scale block
+constexpr int stream32_slab(int mb) {
+    return kStreamSG * 2 * kStreamPlane + mb * 32 * kStreamXRow + (mb + 1) * kStreamSBlock;
+}
+
+// 16 bytes per lane from g into LDS at lds + 16 * lane.  The memory clobber
+// keeps the compiler's LDS reads of the previous chunk ahead of it.
+__device__ __forceinline__ void stream32_dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "m0", "memory");
+}
+__device__ __forceinline__ uint32_t stream32_lds_addr(const void* l) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)l;
+}
 
 // MR: rows folded in the last 32-row activation block (8..32); MB: activation
 // blocks per wavefront (1: M <= 32; 2: 32 < M <= 64, the first block full).
 // Both blocks multiply the same staged weights, so the weights stream once.
-template <int MR, int MB, int KW, int PF, int OCC>
+template <int MR, int MB, int KW, int OCC>
 __global__ __launch_bounds__(64 * KW) __attribute__((amdgpu_waves_per_eu(OCC)))
 void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restrict__ xs,
                              const uint8_t* __restrict__ wq, const uint16_t* __restrict__ ws,
@@ -380,7 +390,7 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq, const uint16_t* __r
                              int groups_per_split) {
     constexpr int NRL = MR / 2;                  // accumulator registers of the last block
     constexpr int NA = 16 * (MB - 1) + NRL;      // accumulator registers in all
-    constexpr int kSlab = kStreamSG * 2 * kStreamPlane;
+    constexpr int kSlab = stream32_slab(MB);
     static_assert(MR % 8 == 0 && MR <= 32 && (MB == 1 || MB == 2), "fold rows");
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -393,7 +403,9 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq, const uint16_t* __r
     const int g_begin = blockIdx.y * groups_per_split;
     const int g_end = min(G, g_begin + groups_per_split);
     const int nst = (g_end - g_begin) / kStreamSG;
-    const int cnt = nst > wave ? (nst - wave + KW - 1) / KW : 0;   // stages of this wavefront
+    const int chunk = (nst + KW - 1) / KW;                     // wavefront w: stages [w chunk, (w+1) chunk)
+    const int s0 = wave * chunk;
+    const int cnt = max(0, min(nst, s0 + chunk) - s0);           // stages of this wavefront
     const int n0 = blockIdx.x * 32;
     uint8_t* slab = smem + (size_t)wave * kSlab;
 
@@ -411,14 +423,36 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq, const uint16_t* __r
         const int r = 8 * j + (lane >> 3);
         woff[j] = (uint32_t)(r < nvalid ? r : 0) * (uint32_t)K2 + (uint32_t)(lane & 7) * 16u;
     }
-    const uint32_t swoff = (uint32_t)(l32 < nvalid ? l32 : 0) * (uint32_t)G;
-    uint32_t xoff[MB], sxoff[MB];
+    uint32_t xoff[MB][4];
 #pragma unroll
-    for (int b = 0; b < MB; ++b) {
-        const int mrow = 32 * b + l32 < M ? 32 * b + l32 : 0;
-        xoff[b] = (uint32_t)mrow * (uint32_t)K2 + (uint32_t)half * 16u;
-        sxoff[b] = (uint32_t)mrow * (uint32_t)G;
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = 32 * b + 8 * j + (lane >> 3);
+            xoff[b][j] = (uint32_t)(r < M ? r : 0) * (uint32_t)K2 + (uint32_t)(lane & 7) * 16u;
+        }
+    uint8_t* xslab = slab + kStreamSG * 2 * kStreamPlane;
+    uint8_t* sslab = xslab + MB * 32 * kStreamXRow;
+    // Scale DMA lanes (instruction j of a block): row (64 j + lane) / SC and
+    // stage (lane % SC) ^ f(row), so that the reader of row r, stage q finds
+    // it at 16 (SC r + (q ^ f(r))) with f(r) = (r / (16 / SC)) % SC: 16
+    // consecutive rows then read distinct banks.
+    constexpr int SC = kStreamSC, NJ = 32 * SC / 64;
+    auto swz = [](int r) { return (r / (16 / SC)) % SC; };
+    uint32_t dsx[MB][NJ], dsw[NJ];
+    int dpc[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int rr = (64 * j + lane) / SC;
+        dpc[j] = (lane % SC) ^ swz(rr);
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            const int r = 32 * b + rr;
+            dsx[b][j] = (uint32_t)(r < M ? r : 0) * (uint32_t)G;
+        }
+        dsw[j] = (uint32_t)(rr < nvalid ? rr : 0) * (uint32_t)G;
     }
+    const int rsw = swz(l32);
 
     float acc[NA];
 #pragma unroll
@@ -428,22 +462,38 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq, const uint16_t* __r
 #pragma unroll
     for (int p = 0; p < 4; ++p) fb[p] = (v4i){0, 0, 0, 0};
 
-    auto stage_of = [&](int i) { return wave + i * KW; };
+    auto stage_of = [&](int i) { return s0 + i; };
+    // scales of stages st .. st + SC - 1 (at most the wavefront's last) into
+    // the slab: each row's 16 SC contiguous bytes
+    auto dma_sc = [&](int st) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int sp = min(st + dpc[j], s0 + cnt - 1) * kStreamSG;
+#pragma unroll
+            for (int b = 0; b < MB; ++b)
+                stream32_dma16(sxbase + dsx[b][j] + sp, stream32_lds_addr(sslab + b * kStreamSBlock + 1024 * j));
+            stream32_dma16(swbase + dsw[j] + sp, stream32_lds_addr(sslab + MB * kStreamSBlock + 1024 * j));
+        }
+    };
+    auto read_sc = [&](int q, Stream32Scales<MB>& C) {
+        const int o = l32 * (16 * SC) + 16 * (q ^ rsw);
+#pragma unroll
+        for (int b = 0; b < MB; ++b) C.sx[b] = *reinterpret_cast<const uint4*>(sslab + b * kStreamSBlock + o);
+        C.sw = *reinterpret_cast<const uint4*>(sslab + MB * kStreamSBlock + o);
+    };
     auto load_w = [&](int st, Stream32Stage<MB>& S) {
         const uint8_t* b = wbase + (size_t)st * (kStreamSG * 16);
 #pragma unroll
         for (int j = 0; j < 4; ++j) S.w[j] = load_nt16(b + woff[j]);
     };
-    auto load_xs = [&](int st, Stream32Stage<MB>& S) {
+    auto load_x = [&](int st, Stream32Stage<MB>& S) {
         const uint8_t* bx = xbase + (size_t)st * (kStreamSG * 16);
 #pragma unroll
-        for (int b = 0; b < MB; ++b) {
+        for (int b = 0; b < MB; ++b)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) S.x[b][t] = *reinterpret_cast<const uint4*>(bx + xoff[b] + t * 32);
-            S.sx[b] = *reinterpret_cast<const uint4*>(sxbase + st * kStreamSG + sxoff[b]);
-        }
-        S.sw = *reinterpret_cast<const uint4*>(swbase + st * kStreamSG + swoff);
+            for (int j = 0; j < 4; ++j) S.x[b][j] = *reinterpret_cast<const uint4*>(bx + xoff[b][j]);
     };
+    // weights and activations of a stage into the slab
     auto to_slab = [&](const Stream32Stage<MB>& S) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -453,16 +503,29 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq, const uint16_t* __r
             *reinterpret_cast<uint2*>(base + (g * 2 + 0) * kStreamPlane) = make_uint2(v.x, v.y);
             *reinterpret_cast<uint2*>(base + (g * 2 + 1) * kStreamPlane) = make_uint2(v.z, v.w);
         }
-    };
-    auto compute = [&](Stream32Stage<MB>& S) {
 #pragma unroll
         for (int b = 0; b < MB; ++b)
 #pragma unroll
-            for (int t = 0; t < kStreamSG / 2; ++t) swap_halves(S.x[b][t]);   // rows >= M: not stored
+            for (int j = 0; j < 4; ++j) {
+                const uint4 v = S.x[b][j];
+                const int row = 8 * j + (lane >> 3), g = lane & 7;
+                uint8_t* base = xslab + (b * 32 + row) * kStreamXRow + g * 8;
+                *reinterpret_cast<uint2*>(base) = make_uint2(v.x, v.y);
+                *reinterpret_cast<uint2*>(base + 64) = make_uint2(v.z, v.w);
+            }
+    };
+    auto compute = [&](const Stream32Scales<MB>& S) {
+        // k-half `half` of groups 2t and 2t+1 of row 32b + l32 (rows >= M: not stored)
+        uint4 xr[MB][kStreamSG / 2];
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int t = 0; t < kStreamSG / 2; ++t)
+                xr[b][t] = *reinterpret_cast<const uint4*>(xslab + (b * 32 + l32) * kStreamXRow + half * 64 + t * 16);
         const uint32_t* sww = &S.sw.x;
         // group g, activation block b: D and the fold factors
         auto issue = [&](int g, int b, v16i& d, v16f& f) {
-            const uint4& xv = S.x[b][g >> 1];
+            const uint4& xv = xr[b][g >> 1];
             uint32_t a0, a1, a2, a3, b0, b1, b2, b3;
             unpack_s4x8_x16((g & 1) ? xv.z : xv.x, a0, a1);
             unpack_s4x8_x16((g & 1) ? xv.w : xv.y, a2, a3);
@@ -509,59 +572,33 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq, const uint16_t* __r
         }
     };
 
-    // PF stages of this wavefront in flight: the next weights reuse a stage's
-    // registers as soon as they sit in the slab, before its MFMAs and fold.
-    Stream32Stage<MB> buf[PF];
-#pragma unroll
-    for (int d = 0; d < PF; ++d)
-        if (d < cnt) {
-            load_w(stage_of(d), buf[d]);
-            load_xs(stage_of(d), buf[d]);
-        }
-    // Steady state: every load is needed (no clamped re-reads, and no
-    // conditional loads in the loop, which would keep stale stage registers
-    // live across it).
-    int i = 0;
-    for (; i + 2 * PF <= cnt; i += PF) {
-#pragma unroll
-        for (int d = 0; d < PF; ++d) {
-            to_slab(buf[d]);
-            load_w(stage_of(i + d + PF), buf[d]);
-            __builtin_amdgcn_sched_barrier(0);
-            compute(buf[d]);
-            load_xs(stage_of(i + d + PF), buf[d]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+    // One stage in flight: the next stage's weights and activations are
+    // requested as soon as this stage's sit in the slab, before its MFMAs and
+    // fold.  The scales of stages 4c .. 4c+3 arrive by DMA, requested after
+    // the last read of the previous chunk's (before stage 4c-1's MFMAs) and
+    // waited for at stage 4c, where nothing else is in flight.
+    Stream32Stage<MB> S;
+    if (cnt > 0) {
+        load_w(stage_of(0), S);
+        load_x(stage_of(0), S);
+        dma_sc(stage_of(0));
     }
-    // Drain: r < 2*PF stages left, the first min(r, PF) of them in buf.  The
-    // buffers are consumed inside each branch, so no stage registers stay
-    // live across a conditional load.
-    const int r = cnt - i;
-    if (r > PF) {
-        // one more pipelined pass; a load past the last stage re-reads it
-#pragma unroll
-        for (int d = 0; d < PF; ++d) {
-            const int nx = min(i + d + PF, cnt - 1);
-            to_slab(buf[d]);
-            load_w(stage_of(nx), buf[d]);
-            __builtin_amdgcn_sched_barrier(0);
-            compute(buf[d]);
-            load_xs(stage_of(nx), buf[d]);
-            __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < cnt; ++i) {
+        Stream32Scales<MB> C;
+        to_slab(S);
+        if (i % SC == 0) WUSH_WAIT_VMCNT(0);       // this chunk's scales have landed
+        const int nx = min(i + 1, cnt - 1);          // past the last stage: the last again (not used)
+        load_w(stage_of(nx), S);
+        load_x(stage_of(nx), S);
+        __builtin_amdgcn_sched_barrier(0);
+        read_sc(i % SC, C);
+        if (i % SC == SC - 1 && i + 1 < cnt) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0): the chunk's last scale reads are done
+            dma_sc(stage_of(i + 1));
         }
-#pragma unroll
-        for (int d = 0; d < PF - 1; ++d)
-            if (d < r - PF) {
-                to_slab(buf[d]);
-                compute(buf[d]);
-            }
-    } else {
-#pragma unroll
-        for (int d = 0; d < PF; ++d)
-            if (d < r) {
-                to_slab(buf[d]);
-                compute(buf[d]);
-            }
+        __builtin_amdgcn_sched_barrier(0);
+        compute(C);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // Sum the KW partial accumulators in wavefront order; wavefront w stores
@@ -589,9 +626,8 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq, const uint16_t* __r
 }
 
 constexpr size_t stream32_smem(int kw, int na) {
-    return (size_t)kw * kStreamSG * 2 * kStreamPlane > (size_t)kw * na * 64 * 4
-               ? (size_t)kw * kStreamSG * 2 * kStreamPlane
-               : (size_t)kw * na * 64 * 4;
+    const size_t slab = (size_t)kw * stream32_slab(na > 16 ? 2 : 1);
+    return slab > (size_t)kw * na * 64 * 4 ? slab : (size_t)kw * na * 64 * 4;
 }
 
 // Sum the split-K partials in slice order and convert to fp16.
@@ -715,30 +751,26 @@ static size_t plan_bytes(const Plan& p, int64_t M, int64_t N, int64_t K) {
 #ifndef WUSH_H16A_MIN_N
 #define WUSH_H16A_MIN_N 8192
 #endif
-// 8 < M <= 32 streaming kernel (gemm_s4_stream32_kernel).  Measured on
-// MI355X against one wavefront per 32-row block: L70 (K=8192, N=57344)
-// M = 16 / 24 / 32: 64 / 70 / 80 us against 67 / 75 / 80; Qwen3-8B FFN
-// (K=4096, N=24576) M = 16 / 32: 15.3 / 19.7 us against 23.0 / 30.0.
-#ifndef WUSH_S32_KW
-#define WUSH_S32_KW 8            // wavefronts per workgroup (= K ways) at M <= 16 and 24 < M
-#endif                           // (L70 M=32: 77.9 us with 8, 80.3 with 4; 2 was slower everywhere)
-#ifndef WUSH_S32_KW24
-#define WUSH_S32_KW24 4          // ... at 16 < M <= 24: 137 VGPRs allow 12 wavefronts per CU, one
-#endif                           // 8-wavefront workgroup (L70 M=24: 69.0 us with 4, 73.0 with 8)
-#ifndef WUSH_S32_PF16
-#define WUSH_S32_PF16 1          // stages in flight per wavefront, M <= 16
+// 8 < M <= 64 streaming kernel (gemm_s4_stream32_kernel).  K ways: 4
+// wavefronts per workgroup on wide weights, 8 on narrow ones (measured on
+// MI355X, M = 32: L70 (K=8192, N=57344) 66 us with 4, 83 with 8; K=N=8192
+// 14.7 with 8, 17.8 with 4; K=28672 N=8192 33.4 with 8, 36.2 with 4; K=4096
+// N=24576 18.5 with 4, 23.4 with 8).  Three wavefronts per SIMD at M <= 32
+// (159-166 VGPRs), two at 32 < M <= 64.
+#ifndef WUSH_S32_KW_WIDE
+#define WUSH_S32_KW_WIDE 4       // wavefronts per workgroup (= K ways) when N > WUSH_S32_WIDE_N
 #endif
-#ifndef WUSH_S32_OCC16
-#define WUSH_S32_OCC16 4         // ... and the wavefronts per SIMD its registers allow
+#ifndef WUSH_S32_KW_NARROW
+#define WUSH_S32_KW_NARROW 8     // ... and otherwise
 #endif
-#ifndef WUSH_S32_PF32
-#define WUSH_S32_PF32 1          // the same for 16 < M <= 32 (L70 M=24: 69.7 us with 1 stage
-#endif                           // and 3 wavefronts per SIMD, 76.7 with 2 and 2)
-#ifndef WUSH_S32_OCC24
-#define WUSH_S32_OCC24 3
+#ifndef WUSH_S32_WIDE_N
+#define WUSH_S32_WIDE_N 16384
 #endif
-#ifndef WUSH_S32_OCC32
-#define WUSH_S32_OCC32 4         // (128 VGPRs either way with the 2-deep group pipeline)
+#ifndef WUSH_S32_OCC
+#define WUSH_S32_OCC 3           // wavefronts per SIMD the registers allow, M <= 32
+#endif
+#ifndef WUSH_S32_OCC64
+#define WUSH_S32_OCC64 2         // ... and at 32 < M <= 64
 #endif
 #ifndef WUSH_S32_MIN_STAGES
 #define WUSH_S32_MIN_STAGES 2    // split K across workgroups only while every wavefront keeps this many stages
@@ -750,22 +782,8 @@ static size_t plan_bytes(const Plan& p, int64_t M, int64_t N, int64_t K) {
 #ifndef WUSH_S32_MAXM
 #define WUSH_S32_MAXM 64         // largest M of the streaming kernel (64: two activation blocks)
 #endif
-#ifndef WUSH_S32_KW64
-#define WUSH_S32_KW64 4          // K ways at 32 < M <= 64 (168 VGPRs: 12 wavefronts per CU)
-#endif                           // when N > 16384 (L70 M=64: 111 us with 4, 130 with 8) ...
-#ifndef WUSH_S32_KW64S
-#define WUSH_S32_KW64S 8         // ... and when N <= 16384 (K=N=8192 M=64: 21.0 us with 8, 25.4 with 4)
-#endif
-#ifndef WUSH_S32_KW64_N
-#define WUSH_S32_KW64_N 16384
-#endif
-#ifndef WUSH_S32_OCC64
-#define WUSH_S32_OCC64 2
-#endif
 constexpr int kStream32MaxM = WUSH_S32_MAXM;
-constexpr int stream32_kw(int mr, int64_t n = 0) {
-    return mr == 24 ? WUSH_S32_KW24 : mr == 64 ? (n > WUSH_S32_KW64_N ? WUSH_S32_KW64 : WUSH_S32_KW64S) : WUSH_S32_KW;
-}
+constexpr int stream32_kw(int64_t n) { return n > WUSH_S32_WIDE_N ? WUSH_S32_KW_WIDE : WUSH_S32_KW_NARROW; }
 constexpr int kStream32Waves = WUSH_S32_WAVES;
 
 // scales16: both scale tensors (and both code tensors) are 16-byte aligned
@@ -789,7 +807,7 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         // at least two stages
         p.cfg = 4; p.tm = 32; p.tn = 32; p.sg = kStreamSG;
         p.mr = M > 32 ? 64 : (int)((M + 7) / 8 * 8);
-        const int kw = stream32_kw(p.mr, N);
+        const int kw = stream32_kw(N);
         const int64_t wgs = (N + 31) / 32;
         int s = 1;
         while (s < 16 && wgs * s * kw < kStream32Waves &&
@@ -870,6 +888,25 @@ static void launch_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq
         xq, xs, wq, ws, y, partial, M, N, K, p.groups_per_split, alpha, alpha_dev);
 }
 
+// The streaming kernel for MR rows in the last of MB activation blocks, with
+// the K ways of wide or narrow weights (p.groups_per_split groups per
+// workgroup along grid.y).
+template <int MR, int MB, int OCC>
+static void launch_stream32(dim3 grid, bool wide, const uint8_t* xq, const uint16_t* xs, const uint8_t* wq,
+                            const uint16_t* ws, uint16_t* y, float* partial, int m, int n, int k, const Plan& p,
+                            hipStream_t stream) {
+    constexpr int NA = 16 * (MB - 1) + MR / 2;
+    if (wide) {
+        constexpr int KW = WUSH_S32_KW_WIDE;
+        gemm_s4_stream32_kernel<MR, MB, KW, OCC><<<grid, 64 * KW, stream32_smem(KW, NA), stream>>>(
+            xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
+    } else {
+        constexpr int KW = WUSH_S32_KW_NARROW;
+        gemm_s4_stream32_kernel<MR, MB, KW, OCC><<<grid, 64 * KW, stream32_smem(KW, NA), stream>>>(
+            xq, xs, wq, ws, y, partial, m, n, k, p.groups_per_split);
+    }
+}
+
 template <bool PT>
 static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                     uint16_t* y, int64_t M, int64_t N, int64_t K, void* workspace, size_t ws_bytes,
@@ -897,49 +934,14 @@ static int run_gemm(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
     }
     if (p.cfg == 4) {
         if constexpr (!PT) {
-            dim3 grid((unsigned)((N + 31) / 32), (unsigned)p.splits);
+            const dim3 grid((unsigned)((N + 31) / 32), (unsigned)p.splits);
+            const bool wide = N > WUSH_S32_WIDE_N;
             switch (p.mr) {
-                case 8: {
-                    constexpr int KW = stream32_kw(8);
-                    gemm_s4_stream32_kernel<8, 1, KW, WUSH_S32_PF16, WUSH_S32_OCC16>
-                        <<<grid, 64 * KW, stream32_smem(KW, 4), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
-                                                                         p.groups_per_split);
-                    break;
-                }
-                case 16: {
-                    constexpr int KW = stream32_kw(16);
-                    gemm_s4_stream32_kernel<16, 1, KW, WUSH_S32_PF16, WUSH_S32_OCC16>
-                        <<<grid, 64 * KW, stream32_smem(KW, 8), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
-                                                                          p.groups_per_split);
-                    break;
-                }
-                case 24: {
-                    constexpr int KW = stream32_kw(24);
-                    gemm_s4_stream32_kernel<24, 1, KW, WUSH_S32_PF32, WUSH_S32_OCC24>
-                        <<<grid, 64 * KW, stream32_smem(KW, 12), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
-                                                                           p.groups_per_split);
-                    break;
-                }
-                case 32: {
-                    constexpr int KW = stream32_kw(32);
-                    gemm_s4_stream32_kernel<32, 1, KW, WUSH_S32_PF32, WUSH_S32_OCC32>
-                        <<<grid, 64 * KW, stream32_smem(KW, 16), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
-                                                                           p.groups_per_split);
-                    break;
-                }
-                default:
-                    if (N > WUSH_S32_KW64_N) {
-                        constexpr int KW = WUSH_S32_KW64;
-                        gemm_s4_stream32_kernel<32, 2, KW, 1, WUSH_S32_OCC64>
-                            <<<grid, 64 * KW, stream32_smem(KW, 32), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
-                                                                               p.groups_per_split);
-                    } else {
-                        constexpr int KW = WUSH_S32_KW64S;
-                        gemm_s4_stream32_kernel<32, 2, KW, 1, WUSH_S32_OCC64>
-                            <<<grid, 64 * KW, stream32_smem(KW, 32), stream>>>(xq, xs, wq, ws, y, partial, m, n, k,
-                                                                               p.groups_per_split);
-                    }
-                    break;
+                case 8: launch_stream32<8, 1, WUSH_S32_OCC>(grid, wide, xq, xs, wq, ws, y, partial, m, n, k, p, stream); break;
+                case 16: launch_stream32<16, 1, WUSH_S32_OCC>(grid, wide, xq, xs, wq, ws, y, partial, m, n, k, p, stream); break;
+                case 24: launch_stream32<24, 1, WUSH_S32_OCC>(grid, wide, xq, xs, wq, ws, y, partial, m, n, k, p, stream); break;
+                case 32: launch_stream32<32, 1, WUSH_S32_OCC>(grid, wide, xq, xs, wq, ws, y, partial, m, n, k, p, stream); break;
+                default: launch_stream32<32, 2, WUSH_S32_OCC64>(grid, wide, xq, xs, wq, ws, y, partial, m, n, k, p, stream); break;
             }
         }
     } else if (p.cfg == 0) {

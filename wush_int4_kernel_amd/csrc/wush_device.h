@@ -297,6 +297,14 @@ __device__ __forceinline__ void unpack_s4x8_x16(uint32_t w, uint32_t& lo, uint32
     hi = w & 0xF0F0F0F0u;
 }
 
+// s_waitcnt vmcnt(n) (n < 64) with the other counters left alone, and a
+// workgroup barrier after this wavefront's LDS operations (no wait on vector
+// memory).  The LDS wait is a builtin, so that the compiler's own wait
+// insertion knows every earlier LDS operation has completed (after an asm
+// wait it still counts them outstanding and waits for later operations too).
+#define WUSH_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+#define WUSH_LDS_BARRIER() do { __builtin_amdgcn_s_waitcnt(0xC07F); asm volatile("s_barrier" ::: "memory"); } while (0)
+
 }  // namespace wush
 
 // Common argument check used by the extern "C" entry points.
