@@ -28,7 +28,10 @@
 // 8 bytes of scales.  Both operands use the same order.
 //
 // Shifts: per row and per column over all of K, from a prologue pass over the
-// scales (each lane half takes half of them).
+// scales that reads whole 128-byte lines (the first batches of codes are
+// already in flight).  With each lane reading 16 bytes of its own row or
+// column per instruction (32 lines touched per instruction) the prologue took
+// 20 us of the 108 at L70 M=64; with whole lines 12.
 #include "gemm_h16_device.h"
 #include "gemm_h16.h"
 #include "setup.h"
@@ -47,8 +50,9 @@ constexpr int kSDepth = 4;                       // batches of loads in flight (
 template <int MB, int NCB, bool A_ALL>
 __device__ __forceinline__ void h16s_wave(const uint8_t* __restrict__ xq, const uint16_t* __restrict__ xs,
                                           const uint8_t* __restrict__ wq, const uint16_t* __restrict__ ws,
-                                          uint16_t* __restrict__ y, int M, int N, int K, int cb0,
-                                          uint8_t (*sA)[MB][kSSlices][64 * 16], int* sh_ea, bool write_ea) {
+                                          uint16_t* __restrict__ y, int M, int N, int K, int cb0, int wave,
+                                          uint8_t (*sA)[MB][kSSlices][64 * 16], uint32_t (*sh_mx)[MB * 32],
+                                          int* sh_ea) {
     const int lane = threadIdx.x & 63;
     const int half = lane >> 5;
     const int l32 = lane & 31;
@@ -91,47 +95,7 @@ __device__ __forceinline__ void h16s_wave(const uint8_t* __restrict__ xq, const 
         return max((uint32_t)m.x, (uint32_t)m.y);
     };
 
-    // Prologue: the shifts.  Lane half h takes the largest |scale| of groups
-    // [h G/2, (h+1) G/2) of its row or column, then the other half's.
-    int ea[MB], eb[NC1];
-    {
-        uint32_t mxa[MB], mxb[NC1];
-#pragma unroll
-        for (int b = 0; b < MB; ++b) mxa[b] = 0;
-#pragma unroll
-        for (int c = 0; c < NCB; ++c) mxb[c] = 0;
-        // byte offset of group h G/2 from the lane's scale offset (which sits
-        // at group 4h)
-        // 8 loads per row and column in flight at a time (indices past the
-        // half clamp to its last 8 scales: a repeated maximum changes nothing)
-        const uint32_t h0 = (uint32_t)half * ((uint32_t)G - 8u);
-        for (int i0 = 0; i0 < G / 2; i0 += 64) {
-            uint4 va[8][MB], vb[8][NC1];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const uint32_t o = h0 + 2u * (uint32_t)min(i0 + 8 * k, G / 2 - 8);
-#pragma unroll
-                for (int b = 0; b < MB; ++b) va[k][b] = ld16(xsb, xso[b] + o);
-#pragma unroll
-                for (int c = 0; c < NCB; ++c) vb[k][c] = ld16(wsb, wso[c] + o);
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-#pragma unroll
-                for (int b = 0; b < MB; ++b) mxa[b] = max(mxa[b], max8(va[k][b]));
-#pragma unroll
-                for (int c = 0; c < NCB; ++c) mxb[c] = max(mxb[c], max8(vb[k][c]));
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < MB; ++b) ea[b] = h16_shift(max(mxa[b], (uint32_t)__shfl_xor((int)mxa[b], 32)));
-#pragma unroll
-        for (int c = 0; c < NCB; ++c) eb[c] = h16_shift(max(mxb[c], (uint32_t)__shfl_xor((int)mxb[c], 32)));
-    }
-    if (write_ea && half == 0) {
-#pragma unroll
-        for (int b = 0; b < MB; ++b) sh_ea[32 * b + l32] = ea[b];
-    }
+    int ea[MB], eb[NC1];                         // shifts (set by the prologue below)
 
     // codes and scales of one batch (activations: the four groups of the
     // lane half's quarter)
@@ -206,6 +170,77 @@ __device__ __forceinline__ void h16s_wave(const uint8_t* __restrict__ xq, const 
         load_a(d, RA[d]);
         load_w(d, R[d]);
     }
+    // (the first batches stream in during the prologue)
+    // Prologue: the shifts, from the largest |scale| of every row and column.
+    // The scan reads whole 128-byte lines: 8 lanes per row or column, lane
+    // l % 8 taking its 16-byte pieces l % 8, l % 8 + 8, ... (P = G / 8 pieces;
+    // an index past the last repeats it).  Rows: the 4 MB groups of 8 rows
+    // are split over the 8 wavefronts (2 / MB wavefronts per group, each
+    // taking every (2 / MB)-th run of 8 pieces); the partial maxima meet in
+    // LDS.  Columns: each column wavefront scans its own 4 groups of 8.
+    const int P = G >> 3;
+    auto max_at = [&](global_cptr<uint8_t> base, uint32_t row_off, int p) {
+        return max8(ld16(base, row_off + 16u * (uint32_t)min(p, P - 1)));
+    };
+    // largest over the 8 lanes of each aligned group
+    auto max_over8 = [](uint32_t v) {
+        v = max(v, (uint32_t)__shfl_xor((int)v, 1));
+        v = max(v, (uint32_t)__shfl_xor((int)v, 2));
+        return max(v, (uint32_t)__shfl_xor((int)v, 4));
+    };
+    {
+        constexpr int kWpg = 2 / MB;                 // wavefronts per row group
+        const int gi = wave % (4 * MB), part = wave / (4 * MB);
+        const int r = min(8 * gi + (lane >> 3), M - 1);
+        const uint32_t ro = (uint32_t)r * (uint32_t)G * 2u;
+        uint32_t m = 0;
+        for (int p0 = 8 * part; p0 < P; p0 += 8 * kWpg * 4) {
+            uint32_t v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = max_at(xsb, ro, p0 + 8 * kWpg * u + (lane & 7));
+#pragma unroll
+            for (int u = 0; u < 4; ++u) m = max(m, v[u]);
+        }
+        m = max_over8(m);
+        if ((lane & 7) == 0) sh_mx[part][8 * gi + (lane >> 3)] = m;
+    }
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+        uint32_t mg[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int col = min(32 * (cb0 + c) + 8 * i + (lane >> 3), N - 1);
+            const uint32_t co = (uint32_t)col * (uint32_t)G * 2u;
+            uint32_t m = 0;
+            for (int p0 = 0; p0 < P; p0 += 32) {
+                uint32_t v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = max_at(wsb, co, p0 + 8 * u + (lane & 7));
+#pragma unroll
+                for (int u = 0; u < 4; ++u) m = max(m, v[u]);
+            }
+            mg[i] = max_over8(m);
+        }
+        // column l32 = 8 i + j: group i's maximum, held by lane 8 j
+        const int src = 8 * (l32 & 7);
+        uint32_t mx = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t v = (uint32_t)__shfl((int)mg[i], src);
+            if ((l32 >> 3) == i) mx = v;
+        }
+        eb[c] = h16_shift(mx);
+    }
+    __syncthreads();                                 // row maxima
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int k = 0; k < 2 / MB; ++k) m = max(m, sh_mx[k][32 * b + l32]);
+        ea[b] = h16_shift(m);
+        if (wave == 0 && half == 0) sh_ea[32 * b + l32] = ea[b];
+    }
+
     convert_a(RA[0], 0);
     load_a(D, RA[0]);
     __syncthreads();                             // sh_ea, activation batch 0
@@ -282,12 +317,13 @@ void gemm_h16s_kernel(const uint8_t* __restrict__ xq, const uint16_t* __restrict
                       int M, int N, int K) {
     // activation operands of a batch: [buffer][row block][slice][lane][16 B]
     __shared__ __align__(16) uint8_t sA[2][MB][kSSlices][64 * 16];
+    __shared__ uint32_t sh_mx[2][MB * 32];
     __shared__ int sh_ea[MB * 32];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (wave == kSCols)
-        h16s_wave<MB, 0, true>(xq, xs, wq, ws, y, M, N, K, 0, sA, sh_ea, false);
+        h16s_wave<MB, 0, true>(xq, xs, wq, ws, y, M, N, K, 0, wave, sA, sh_mx, sh_ea);
     else
-        h16s_wave<MB, 1, false>(xq, xs, wq, ws, y, M, N, K, blockIdx.x * kSCols + wave, sA, sh_ea, wave == 0);
+        h16s_wave<MB, 1, false>(xq, xs, wq, ws, y, M, N, K, blockIdx.x * kSCols + wave, wave, sA, sh_mx, sh_ea);
 }
 
 template <int MB>
