@@ -160,13 +160,17 @@ def ref_reps(M: int) -> int:
     return 100 if M <= 8 else (30 if M <= 64 else 8)
 
 
-def prefill_mfma(M: int, K: int) -> str:
+def prefill_mfma(M: int, N: int, K: int) -> str:
     """MFMA type of the w4a4_gemm_s4 kernel for M rows at the bench's shapes:
     the fp16 tiles from M = 256 when K % 256 == 0 (every bench shape has at
     least 16 column tiles of 256, which with M >= 256 meets the planner's
-    tile-count condition, except Qwen3-8B K=N=4096 below M = 2048), int8
-    otherwise."""
-    return "fp16" if M >= 256 and K % 256 == 0 else "int8"
+    tile-count condition, except Qwen3-8B K=N=4096 below M = 2048), the fp16
+    streaming kernel at 32 < M <= 64 when 224 to 256 workgroups of 224
+    columns cover N and K % 1024 == 0, int8 otherwise."""
+    wgs = -(-N // 224)
+    if (M >= 256 and K % 256 == 0) or (32 < M <= 64 and 224 <= wgs <= 256 and K % 1024 == 0):
+        return "fp16"
+    return "int8"
 
 
 SWEEP_SHAPES = [("Qwen3-8B", 4096, 4096), ("Qwen3-8B", 4096, 24576), ("Qwen3-8B", 12288, 4096),
@@ -453,7 +457,7 @@ def main():
         reps12 = max(1, -(-args.steps // gs)) if M <= 64 else 1
         t12 = time_med5(chain_graph(gs), gs, reps12)
         t1 = time_med5(chain_graph(1), 1, ref_reps(M))
-        mfma = prefill_mfma(M, K)
+        mfma = prefill_mfma(M, N, K)
         peak = FP16_PEAK_TFLOPS if mfma == "fp16" else INT8_PEAK_TOPS
         tflops = 2 * M * N * K / t_int4 / 1e12
         entry = {
