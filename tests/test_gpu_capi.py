@@ -542,6 +542,30 @@ def test_gemm_stream_k_split_shapes(capi, M, N, K):
     assert rel_fro(y, ref) < FRO_TOL, (M, N, K, rel_fro(y, ref))
 
 
+@pytest.mark.parametrize("M,N,K,groups", [
+    # wide weights (4 K ways): 40 stages in runs of 10 per wavefront, so the
+    # scale chunks of 4 stages start at stages 0, 4, 8 of a run, the last one
+    # clamped; groups at run, chunk and stage boundaries
+    (24, 16416, 10240, [0, 31, 32, 63, 64, 72, 79, 80, 239, 240, 319]),
+    # 9 stages: runs of 3, 3, 3 and an idle wavefront; ragged last column block
+    (9, 16400, 2304, [0, 7, 8, 23, 24, 47, 48, 71]),
+])
+def test_gemm_stream_wide_exact_per_group(capi, M, N, K, groups):
+    # The streaming kernel on wide weights: scales 1 on group g only and 0
+    # elsewhere -> y = D[:, :, g] exactly, wherever the stage of g falls in
+    # its wavefront's run and in its 4-stage scale chunk.
+    g = rng(4290 + M)
+    xq, _, wq, _ = _rand_operands(g, M, N, K)
+    for gg in groups:
+        D = oracle.group_dots(xq[:, 16 * gg:16 * gg + 16], wq[:, 16 * gg:16 * gg + 16])[:, :, 0]
+        xs = np.zeros((M, K // 32), np.uint16)
+        ws = np.zeros((N, K // 32), np.uint16)
+        xs[:, gg] = 0x3F80
+        ws[:, gg] = 0x3F80
+        y = run_gemm(capi, xq, xs, wq, ws)
+        assert np.array_equal(y, D.astype(np.float64)), (M, N, K, gg)
+
+
 def test_gemm_random_shapes_all_paths(capi):
     # Seeded random shapes over every planner branch: the streaming kernel
     # (K % 256 == 0, M <= 64, with and without split-K), the LDS tiles (other
