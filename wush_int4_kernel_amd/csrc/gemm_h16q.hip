@@ -17,7 +17,11 @@
 // fragments, the conversion of stage t+1's weights, the DMAs of stage t+4.
 // One barrier per stage.  A wavefront's weight codes come in batches of four
 // stages, DMA'd into LDS two batches ahead and read into registers once per
-// batch (6 LDS reads per 4 stages, not 4 per stage: 4% faster at L70).
+// batch (6 LDS reads per 4 stages, not 4 per stage: 4% faster at L70).  The
+// codes are DMA'd two batches at a time, each column's whole 128-byte line
+// per 8 lanes: with 32 bytes of 32 columns per DMA the kernel took 2-4%
+// longer (a load touching 32 lines costs the vector memory path about as much
+// as one reading them whole).
 //
 // Every global load of the kernel is an LDS DMA issued by an asm statement
 // (activations, weight codes and scales, shifts), and the kernel orders them
@@ -82,10 +86,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ ea, const int* __restrict__ eb,
                       const uint8_t* __restrict__ wq, const uint16_t* __restrict__ ws, uint16_t* __restrict__ y,
                       float* __restrict__ partial, int M, int N, int K, int groups_per_split, int splits) {
-    // activation ring (4 stages) and, per wavefront, two weight batches of 4
-    // stages: codes [4 loads][64 lanes][16 B], scales [2 columns][64 lanes][4 B]
+    // activation ring (4 stages) and, per wavefront, two double batches of
+    // weight codes [64 columns][128 B, pieces swizzled] and two batches of
+    // scales [2 columns][64 lanes][4 B]
     __shared__ __align__(16) uint8_t sA[4][kH16Op];
-    __shared__ __align__(16) uint8_t sBc[2][4][4096];
+    __shared__ __align__(16) uint8_t sBc[2][4][8192];
     __shared__ __align__(16) uint32_t sBs[2][4][128];
     __shared__ __align__(16) int sh_e[512];      // [0, 256) rows, [256, 512) columns
 
@@ -122,26 +127,36 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
         dma16(src + arb, dst + 1024);
         dma16(src + arb + 1024, dst + kH16Slice + 1024);
     };
-    // this lane's two weight columns (blocks 2w and 2w + 1) and code half
+    // this lane's two weight columns (blocks 2w and 2w + 1): their scales
     const int colA = min(n0 + wave * 64 + l32, limn);
     const int colB = min(n0 + wave * 64 + 32 + l32, limn);
-    const uint8_t* qa = wq + (size_t)colA * K2 + gb * 16 + half * 32;
-    const uint8_t* qb = wq + (size_t)colB * K2 + gb * 16 + half * 32;
     const uint16_t* sa = ws + (size_t)colA * GR + gb + 2 * half;
     const uint16_t* sb = ws + (size_t)colB * GR + gb + 2 * half;
-    constexpr int kB = 6;                        // DMAs of one weight batch
-    auto issue_b = [&](int b, int buf) {
+    // Weight codes come in double batches (8 groups, each column's whole
+    // 128-byte line): DMA k of a double batch reads columns 8k .. 8k+7 of the
+    // wavefront's 64, 8 lanes a line.  Lane l fetches piece (l % 8) ^ f(c) of
+    // column c = 8k + l / 8, so that piece p of column c sits at
+    // 128 c + 16 (p ^ f(c)) with f(c) = (c / 2) % 8: 16 consecutive readers
+    // (columns c .. c+15, one piece) hit distinct banks.
+    const uint32_t cbase = (uint32_t)(n0 + wave * 64);
+    auto issue_db = [&](int d, int buf) {
+        const int o = min(d * 2 * kH16Batch, G - 2 * kH16Batch);
+        const uint8_t* base = wq + (size_t)(gb + o) * 16;
+        const uint32_t c0 = lds_addr(sBc[buf][wave]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int c = 8 * k + (lane >> 3);
+            const int p = (lane & 7) ^ ((c >> 1) & 7);
+            const uint32_t col = min(cbase + (uint32_t)c, (uint32_t)limn);
+            dma16(base + (size_t)col * K2 + p * 16, c0 + 1024 * k);
+        }
+    };
+    auto issue_s = [&](int b, int buf) {
         const int o = min(b * kH16Batch, G - kH16Batch);
-        const uint32_t c = lds_addr(sBc[buf][wave]);
-        dma16(qa + o * 16, c);
-        dma16(qa + o * 16 + 16, c + 1024);
-        dma16(qb + o * 16, c + 2048);
-        dma16(qb + o * 16 + 16, c + 3072);
         const uint32_t s = lds_addr(sBs[buf][wave]);
         dma4(sa + o, s);
         dma4(sb + o, s + 256);
     };
-
     v16f acc[8][2];
     h8 fa[2][2][8];                              // [register set][K16 slice][row block]
     h8 fb[2][2][2];                              // [register set][K16 slice][column block]
@@ -157,12 +172,19 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
         u32x4 c[2][2];                           // [column block][16-byte half]
         uint32_t s[2];
     };
-    auto read_batch = [&](int buf, Batch& r) {
+    // batch b: double batch b / 2 in code buffer (b / 2) & 1, its half b & 1;
+    // scales in buffer b & 1
+    const int fsw = (l32 >> 1) & 7;                // f(c) of both the lane's columns
+    auto read_batch = [&](int b, Batch& r) {
+        const uint8_t* cb = sBc[(b >> 1) & 1][wave];
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
-            r.c[k >> 1][k & 1] = *reinterpret_cast<const u32x4*>(sBc[buf][wave] + k * 1024 + lane * 16);
-        r.s[0] = sBs[buf][wave][lane];
-        r.s[1] = sBs[buf][wave][64 + lane];
+        for (int k = 0; k < 4; ++k) {
+            const int c = (k >> 1) * 32 + l32;       // column block A, then B
+            const int p = 4 * (b & 1) + 2 * half + (k & 1);
+            r.c[k >> 1][k & 1] = *reinterpret_cast<const u32x4*>(cb + c * 128 + 16 * (p ^ fsw));
+        }
+        r.s[0] = sBs[b & 1][wave][lane];
+        r.s[1] = sBs[b & 1][wave][64 + lane];
     };
     // stage s (0-3) of a batch, column block jb -> B operands of register set P
     auto convert_b = [&](int P, const Batch& r, int s, int jb) {
@@ -182,9 +204,10 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
     issue_a(1, 1);
     issue_a(2, 2);
     issue_a(3, 3);
-    issue_b(0, 0);
-    issue_b(1, 1);
-    WUSH_WAIT_VMCNT(kB);                         // all but batch 1
+    issue_db(0, 0);
+    issue_s(0, 0);
+    issue_s(1, 1);
+    WUSH_WAIT_VMCNT(2);                          // all but batch 1's scales
     WUSH_LDS_BARRIER();
     eA = sh_e[256 + wave * 64 + l32];
     eB = sh_e[256 + wave * 64 + 32 + l32];
@@ -208,15 +231,20 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
             const int P = j & 1;
             issue_a(t + 4, j & 3);               // into the slot stage t left
             // a batch buffer's next batch once its last stage is converted
-            if (j == 3) issue_b(s0 / kH16Batch + 2, 0);
-            if (j == 7) issue_b(s0 / kH16Batch + 3, 1);
+            // double batch s0 / 8 + 1 once batch s0 / 4 - 1 (its buffer's
+            // last) is in registers; batch scales as before
+            if (j == 3) {
+                issue_db(s0 / (2 * kH16Batch) + 1, (s0 / (2 * kH16Batch) + 1) & 1);
+                issue_s(s0 / kH16Batch + 2, 0);
+            }
+            if (j == 7) issue_s(s0 / kH16Batch + 3, 1);
             // stage t + 1's weights: batch (t + 1) / 4, in LDS buffer
             // ((t + 1) / 4) & 1, stage (j + 1) % 4 of it.  A batch goes into
             // registers at the stage before its first, ahead of that stage's
             // fragment reads (LDS returns in order: read late, the
             // conversion would wait for all of them).
-            if (j == 3) read_batch(1, R1);
-            if (j == 7) read_batch(0, R0);
+            if (j == 3) read_batch(s0 / kH16Batch + 1, R1);
+            if (j == 7) read_batch(s0 / kH16Batch + 2, R0);
             const Batch& Rc = (j < 3 || j == 7) ? R0 : R1;
             const int sc = (j + 1) & 3;
             // 32 MFMAs of stage t; between them stage t+1's 16 activation
@@ -253,10 +281,12 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
             // stage t+3's and t+4's (8) plus the batches of stages t-2 .. t
             // (issued after their stage's activations); at the first stages
             // the count also covers the prologue's DMAs
-            const int nb = (j == 3 || j == 7) + (j == 4 || j == 0) + (j == 5 || j == 1);
+            // (10 weight DMAs at j = 3, 2 at j = 7)
+            const int nb = (j >= 3 && j <= 5) ? 10 : (j == 7 || j <= 1) ? 2 : 0;
             __builtin_amdgcn_sched_barrier(0);
             if (nb == 0) WUSH_WAIT_VMCNT(8);
-            else WUSH_WAIT_VMCNT(8 + kB);
+            else if (nb == 2) WUSH_WAIT_VMCNT(10);
+            else WUSH_WAIT_VMCNT(18);
             WUSH_LDS_BARRIER();
             __builtin_amdgcn_sched_barrier(0);
         }
