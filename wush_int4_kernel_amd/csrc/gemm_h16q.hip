@@ -51,18 +51,6 @@ namespace {
 #define WUSH_H16Q_SCHED 1                        // explicit MFMA / LDS / VALU interleave
 #endif
 
-// LDS address (wave-uniform) of a __shared__ pointer
-__device__ __forceinline__ uint32_t lds_addr(const void* l) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)l;
-}
-// 16 (4) bytes per lane from g into LDS at lds + 16 (4) * lane
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "m0");
-}
-__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(g), "s"(lds) : "m0");
-}
-
 // Tile id -> (row tile, column tile): workgroup i runs on XCD i % 8.  Each
 // XCD walks its column tiles in groups of 8, all row tiles of a group before
 // the next, so the workgroups in flight on an XCD share 8 weight column

@@ -370,15 +370,6 @@ constexpr int stream32_slab(int mb) {
     return kStreamSG * 2 * kStreamPlane + mb * 32 * kStreamXRow + (mb + 1) * kStreamSBlock;
 }
 
-// 16 bytes per lane from g into LDS at lds + 16 * lane.  The memory clobber
-// keeps the compiler's LDS reads of the previous chunk ahead of it.
-__device__ __forceinline__ void stream32_dma16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "m0", "memory");
-}
-__device__ __forceinline__ uint32_t stream32_lds_addr(const void* l) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)l;
-}
-
 // MR: rows folded in the last 32-row activation block (8..32); MB: activation
 // blocks per wavefront (1: M <= 32; 2: 32 < M <= 64, the first block full).
 // Both blocks multiply the same staged weights, so the weights stream once.
@@ -471,8 +462,8 @@ void gemm_s4_stream32_kernel(const uint8_t* __restrict__ xq, const uint16_t* __r
             const int sp = min(st + dpc[j], s0 + cnt - 1) * kStreamSG;
 #pragma unroll
             for (int b = 0; b < MB; ++b)
-                stream32_dma16(sxbase + dsx[b][j] + sp, stream32_lds_addr(sslab + b * kStreamSBlock + 1024 * j));
-            stream32_dma16(swbase + dsw[j] + sp, stream32_lds_addr(sslab + MB * kStreamSBlock + 1024 * j));
+                dma16_ordered(sxbase + dsx[b][j] + sp, lds_addr(sslab + b * kStreamSBlock + 1024 * j));
+            dma16_ordered(swbase + dsw[j] + sp, lds_addr(sslab + MB * kStreamSBlock + 1024 * j));
         }
     };
     auto read_sc = [&](int q, Stream32Scales<MB>& C) {

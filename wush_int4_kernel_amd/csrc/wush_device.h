@@ -297,6 +297,24 @@ __device__ __forceinline__ void unpack_s4x8_x16(uint32_t w, uint32_t& lo, uint32
     hi = w & 0xF0F0F0F0u;
 }
 
+// LDS address (wave-uniform) of a __shared__ pointer
+__device__ __forceinline__ uint32_t lds_addr(const void* l) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)l;
+}
+// LDS DMA: 16 (4) bytes per lane from g into LDS at lds + 16 (4) * lane.
+// The compiler does not count these in its vmcnt waits: a caller waits for
+// them itself (WUSH_WAIT_VMCNT) and keeps its own LDS reads of the target in
+// order (sched_barrier, or the memory clobber of dma16_ordered).
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(g), "s"(lds) : "m0");
+}
+__device__ __forceinline__ void dma16_ordered(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds) : "m0", "memory");
+}
+
 // s_waitcnt vmcnt(n) (n < 64) with the other counters left alone, and a
 // workgroup barrier after this wavefront's LDS operations (no wait on vector
 // memory).  The LDS wait is a builtin, so that the compiler's own wait
