@@ -242,6 +242,47 @@ def test_fused_extreme_operands_both_loops(capi, rows):
     assert np.array_equal(s, so), np.argwhere(s != so)[:5]
 
 
+def _takes_two_tile(rows: int, K: int, cus: int) -> bool:
+    """Whether wush_fused_tq runs a (rows, K) launch on the two-tile rows kernel:
+    more than 16384 (row, block) pairs, at least 2 of its 128-row workgroups
+    per CU, and no CU with more tiles than the 64-row kernel would give it."""
+    C = K // 32
+    gx, gy, gy2 = -(-C // 4), -(-rows // 64), -(-rows // 128)
+    per_cu1, per_cu2 = -(-gx * gy // cus), -(-gx * gy2 // cus)
+    return rows * C > 16384 and gx * gy2 >= 2 * cus and 2 * per_cu2 <= per_cu1
+
+
+# The two-tile rows kernel (two 64-row tiles per wavefront).  Shapes: cfg2's
+# 2048 x 4096, partial 128-row and 4-block sets (3900 x 4128), and a last
+# workgroup with a partial first tile and an empty second one (32691 x 256).
+# The last shape plants out-of-range values in the first tile only, the second
+# only, or neither, of a workgroup's blocks (and in some T blocks), so the
+# MFMA steps, the fma loop and the mul-then-add loop meet in every pairing.
+@pytest.mark.parametrize("rows,K,special", [(2048, 4096, False), (3900, 4128, False), (32691, 256, True)])
+def test_fused_two_tile_kernel(capi, rows, K, special):
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if not _takes_two_tile(rows, K, cus):
+        pytest.skip(f"{rows} x {K} does not take the two-tile kernel on {cus} CUs")
+    g = rng(2100 + rows + K)
+    xb = outlier_activations(g, rows, K)
+    tb = f32_to_bf16_bits(g.standard_normal((K // 32, 32, 32)) * 0.25)
+    if special:
+        specials = [0x0001, 0x8001, 0x1DFF, 0x1E00, 0x5900, 0x7F80, 0xFF80, 0x7FC0, 0x237F, 0x2000]
+        for wg in range(-(-rows // 128)):
+            for blk in g.choice(K // 32, size=3, replace=False):
+                half = (wg + blk) % 3                  # 0: first tile, 1: second tile, 2: neither
+                r = wg * 128 + 64 * half + int(g.integers(0, 64))
+                if half < 2 and r < rows:
+                    xb[r, blk * 32 + int(g.integers(0, 32))] = specials[(wg + blk) % len(specials)]
+        tb[1, 3, 5] = 0x0001                           # whole blocks: mul-then-add
+        tb[5, 2, 30] = 0x237F                          # fma loop
+    q, s = run_fused(capi, xb, tb)
+    qo, so = oracle.fused_tq(xb, tb)
+    assert np.array_equal(q, qo), (rows, K, np.argwhere(q != qo)[:5])
+    assert np.array_equal(s, so), (rows, K, np.argwhere(s != so)[:5])
+
+
 def run_transform32(capi, xb: np.ndarray, tb: np.ndarray) -> np.ndarray:
     import torch
     rows = xb.shape[0]

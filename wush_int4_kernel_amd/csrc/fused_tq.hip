@@ -26,6 +26,7 @@
 //    re-run in i-order by every lane from LDS (so they keep the sequential
 //    order) and lane pairs pack nibbles.
 #include "fused_tq_device.h"
+#include "setup.h"
 #include "../../include/wush_int4.h"
 
 namespace wush {
@@ -101,20 +102,17 @@ constexpr uint32_t kMfmaSafeLo = 0x2380u;        // bf16 magnitude bits of 2^-56
 
 typedef float v32f __attribute__((ext_vector_type(32)));
 
-// x'_j of the wavefront's 64 rows in xp (lane = row): the 32 MFMA steps, T
-// converted to fp32 as it is used, then the regrouping.  Block k's output is
+// x'_j of the wavefront's 64 rows in xp (lane = row): the 32 MFMA steps on
+// tf (the lane's row l % 32 of T[c] in fp32), then the regrouping.  Block k's output is
 // in registers 16k .. 16k + 15: lane l, register e holds n = l % 32 and m =
 // 8 (e / 4) + 4 (l / 32) + e % 4.  Swapping block 1's registers of lanes 0-31
 // with block 0's of lanes 32-63 leaves lane l with all 32 x'_j of row r0 + l:
 // j = 8a + b from the first register of the pair, 8a + 4 + b from the second
 // (e = 4a + b).
-__device__ __forceinline__ void tq_mfma_steps(const uint32_t (&ut)[16], const float (&xv)[32], float (&xp)[32]) {
+__device__ __forceinline__ void tq_mfma_steps_f32(const float (&tf)[32], const float (&xv)[32], float (&xp)[32]) {
     v32f acc = (v32f){0.0f};
 #pragma unroll
-    for (int d = 0; d < 16; ++d) {
-        acc = __builtin_amdgcn_mfma_f32_32x32x1f32(bf16_to_f32(ut[d] & 0xffffu), xv[2 * d], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x1f32(__uint_as_float(ut[d] & 0xffff0000u), xv[2 * d + 1], acc, 0, 0, 0);
-    }
+    for (int i = 0; i < 32; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x1f32(tf[i], xv[i], acc, 0, 0, 0);
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[e]), __float_as_uint(acc[16 + e]),
@@ -149,7 +147,15 @@ __device__ __forceinline__ void tq_rows_transform(const uint32_t (&ux)[16], cons
         rg.add(ux[d]);
         rg.add(ut[d]);
     }
-    if (__all(rg.safe_from(kMfmaSafeLo))) tq_mfma_steps(ut, xv, xp);
+    if (__all(rg.safe_from(kMfmaSafeLo))) {
+        float tf[32];
+#pragma unroll
+        for (int d = 0; d < 16; ++d) {
+            tf[2 * d] = bf16_to_f32(ut[d] & 0xffffu);
+            tf[2 * d + 1] = __uint_as_float(ut[d] & 0xffff0000u);
+        }
+        tq_mfma_steps_f32(tf, xv, xp);
+    }
     else if (__all(rg.safe())) transform_block<true>(xv, tc, xp);
     else transform_block<false>(xv, tc, xp);
 }
@@ -253,6 +259,138 @@ __global__ __launch_bounds__(256) void fused_tq_rows_kernel(const uint16_t* __re
     }
 }
 
+// Two 64-row tiles per wavefront (128 rows x 4 blocks per workgroup): the
+// rows kernel's steps, with the wavefront's T row requested first, converted
+// to fp32 and range-checked once for both tiles, and both tiles' input
+// requested before the first tile's transform.  On gfx950 the fp32 MFMA
+// steps and the VALU do not run at the same time (not in one wavefront, not
+// across the wavefronts of a SIMD), so the tiles simply run one after the
+// other; the gain is the shared T work and its hidden latency.  Launched
+// where its 128-row workgroups leave no CU with more tiles than the rows
+// kernel's 64-row ones would.
+constexpr int kRows2 = 2 * kRowsPerWave;
+
+__global__ __launch_bounds__(256) void fused_tq_rows2_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ t,
+                                                             uint8_t* __restrict__ q,
+                                                             uint16_t* __restrict__ s,
+                                                             int64_t rows, int64_t K) {
+    __shared__ __align__(16) uint8_t sx[kRows2 * kTqXPitch];
+    __shared__ __align__(16) uint8_t sq[kRows2 * kTqQPitch];
+    __shared__ __align__(16) uint16_t ss[kRows2 * kBlocksPerWg];
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int64_t C = K >> 5;
+    const int64_t cb = (int64_t)blockIdx.x * kBlocksPerWg;
+    const int64_t r0 = (int64_t)blockIdx.y * kRows2;
+    const bool full = r0 + kRows2 <= rows && cb + kBlocksPerWg <= C && K < ((int64_t)1 << 28);
+
+    // row lane % 32 of this wavefront's T[c], the MFMA's A operand for both tiles
+    const int64_t c = min(cb + wave, C - 1);
+    const uint32_t* tc = reinterpret_cast<const uint32_t*>(t + c * 1024);
+    uint32_t ut[16];
+    {
+        const uint4* t4 = reinterpret_cast<const uint4*>(tc + (lane & 31) * 16);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint4 a = t4[k];
+            ut[4 * k] = a.x; ut[4 * k + 1] = a.y; ut[4 * k + 2] = a.z; ut[4 * k + 3] = a.w;
+        }
+    }
+    // both tiles' input, coalesced: wavefront w loads rows 16w .. 16w + 15 of each
+    u32x4 vin[2][4];
+    if (full) {
+        uint32_t lo = ((uint32_t)(lane >> 4) * (uint32_t)K + (uint32_t)(lane & 15) * 8u) * 2u;
+        asm("" : "+v"(lo));                      // keeps the 32-bit lane offset form
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const global_cptr<uint8_t> xb = uniform_ptr(
+                reinterpret_cast<const uint8_t*>(x + (r0 + kRowsPerWave * h + 16 * wave) * K + cb * 32));
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                vin[h][k] = *reinterpret_cast<global_cptr<u32x4>>(xb + (size_t)(8 * k) * (size_t)K + lo);
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int rl = kRowsPerWave * h + 16 * wave + 4 * k + (lane >> 4);
+                const int64_t rr = min(r0 + rl, rows - 1);
+                const int64_t cc = min(cb + ((lane & 15) >> 2), C - 1);
+                const uint4 v = *reinterpret_cast<const uint4*>(x + rr * K + cc * 32 + (lane & 3) * 8);
+                vin[h][k] = (u32x4){v.x, v.y, v.z, v.w};
+            }
+    }
+    float tf[32];
+    BfRange rg_t;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+        tf[2 * d] = bf16_to_f32(ut[d] & 0xffffu);
+        tf[2 * d + 1] = __uint_as_float(ut[d] & 0xffff0000u);
+        rg_t.add(ut[d]);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        // tile h through LDS (rows 64h ..; tile 0's rows are not written again)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            *reinterpret_cast<u32x4*>(sx + (kRowsPerWave * h + 16 * wave + 4 * k + (lane >> 4)) * kTqXPitch +
+                                      (lane & 15) * 16) = vin[h][k];
+        __syncthreads();
+        uint32_t ux[16];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint4 v = *reinterpret_cast<const uint4*>(sx + (kRowsPerWave * h + lane) * kTqXPitch + wave * 64 +
+                                                            k * 16);
+            ux[4 * k] = v.x; ux[4 * k + 1] = v.y; ux[4 * k + 2] = v.z; ux[4 * k + 3] = v.w;
+        }
+        float xv[32];
+        BfRange rg = rg_t;
+#pragma unroll
+        for (int d = 0; d < 16; ++d) {
+            xv[2 * d] = bf16_to_f32(ux[d] & 0xffffu);
+            xv[2 * d + 1] = __uint_as_float(ux[d] & 0xffff0000u);
+            rg.add(ux[d]);
+        }
+        float xp[32];
+        if (__all(rg.safe_from(kMfmaSafeLo))) tq_mfma_steps_f32(tf, xv, xp);
+        else if (__all(rg.safe())) transform_block<true>(xv, tc, xp);
+        else transform_block<false>(xv, tc, xp);
+        uint32_t w[4];
+        const uint32_t sb = quant_group32(xp, w);
+        *reinterpret_cast<uint4*>(sq + (kRowsPerWave * h + lane) * kTqQPitch + wave * 16) =
+            make_uint4(w[0], w[1], w[2], w[3]);
+        ss[(kRowsPerWave * h + lane) * kBlocksPerWg + wave] = (uint16_t)sb;
+    }
+    __syncthreads();
+
+    // coalesced output: wavefront w stores rows 32w .. 32w + 31, 16 a pass, 4 lanes a row
+    const int bl = lane & 3;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int rl = 32 * wave + 16 * p + (lane >> 2);
+        const u32x4 qv = *reinterpret_cast<const u32x4*>(sq + rl * kTqQPitch + bl * 16);
+        const uint16_t sv = ss[rl * kBlocksPerWg + bl];
+        if (full) {
+            const int64_t e0 = (r0 + 32 * wave + 16 * p) * C + cb;
+            const global_ptr<uint8_t> qb = uniform_wptr(q + e0 * 16);
+            const global_ptr<uint16_t> sp = uniform_wptr(s + e0);
+            uint32_t eo = (uint32_t)(lane >> 2) * (uint32_t)C + (uint32_t)bl;
+            asm("" : "+v"(eo));
+            *reinterpret_cast<global_ptr<u32x4>>(qb + eo * 16u) = qv;
+            sp[eo] = sv;
+        } else {
+            const int64_t r = r0 + rl, cs = cb + bl;
+            if (r < rows && cs < C) {
+                *reinterpret_cast<u32x4*>(q + (r * C + cs) * 16) = qv;
+                s[r * C + cs] = sv;
+            }
+        }
+    }
+}
+
 // The transform stage alone, for one block: x rows x 32, xp rows x 32 fp32.
 __global__ __launch_bounds__(64) void fused_tq_transform32_kernel(const uint16_t* __restrict__ x,
                                                                   const uint16_t* __restrict__ t,
@@ -306,6 +444,11 @@ __global__ __launch_bounds__(64) void fused_tq_smallm_kernel(const uint16_t* __r
 // Launches of at most this many (row, block) pairs use the small-M kernel,
 // whose time grows with the pairs from a lower floor than the rows kernel's
 // (K=4096: 64 rows 4.1 vs 6.0 us, 128 rows 5.7 vs 5.9 us, 256 rows 9.0 vs 6.2 us).
+// Smallest number of two-tile workgroups per CU at which the rows launches
+// may take the two-tile kernel (a large value: never).
+#ifndef WUSH_TQ_ROWS2_MIN_PER_CU
+#define WUSH_TQ_ROWS2_MIN_PER_CU 2
+#endif
 #ifndef WUSH_TQ_SMALLM_PAIRS
 #define WUSH_TQ_SMALLM_PAIRS 16384
 #endif
@@ -326,9 +469,22 @@ extern "C" int wush_fused_tq(const uint16_t* x, const uint16_t* t, uint8_t* q, u
     } else {
         const int64_t gx = (C + wush::kBlocksPerWg - 1) / wush::kBlocksPerWg;
         const int64_t gy = (rows + wush::kRowsPerWave - 1) / wush::kRowsPerWave;
+        const int64_t gy2 = (rows + wush::kRows2 - 1) / wush::kRows2;
         WUSH_REQUIRE(gx <= 0x7fffffffLL && gy <= 65535);
-        const dim3 grid((unsigned)gx, (unsigned)gy);
-        wush::fused_tq_rows_kernel<<<grid, 256, 0, stream>>>(x, t, q, s, rows, K);
+        int dev = 0;
+        const int st = wush::device_setup(&dev);
+        if (st != 0) return st;
+        // the two-tile kernel where no CU gets more tiles than with the rows
+        // kernel (workgroups spread evenly over the CUs), at least 2
+        // workgroups per CU
+        const int64_t cus = wush::device_cus(dev);
+        const int64_t per_cu1 = (gx * gy + cus - 1) / cus, per_cu2 = (gx * gy2 + cus - 1) / cus;
+        if (gx * gy2 >= WUSH_TQ_ROWS2_MIN_PER_CU * cus && 2 * per_cu2 <= per_cu1) {
+            wush::fused_tq_rows2_kernel<<<dim3((unsigned)gx, (unsigned)gy2), 256, 0, stream>>>(x, t, q, s, rows, K);
+        } else {
+            const dim3 grid((unsigned)gx, (unsigned)gy);
+            wush::fused_tq_rows_kernel<<<grid, 256, 0, stream>>>(x, t, q, s, rows, K);
+        }
     }
     return (int)hipGetLastError();
 }

@@ -19,6 +19,9 @@ int device_setup(int* dev);
 int gemm_h16_init_device();                      // gemm_h16.hip: dynamic LDS limit
 int gemv_init_device(int dev);                   // gemv.hip: occupancy table
 
+// Compute units of device `dev` (256 before a successful device_setup on it).
+int device_cus(int dev);
+
 // Device address of the static split-K scratch array on device `dev`
 // (WUSH_GEMM_SCRATCH_BYTES), looked up by device_setup; only valid after a
 // successful device_setup on that device.

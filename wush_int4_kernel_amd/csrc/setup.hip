@@ -22,6 +22,7 @@ int g_status[kMaxDevices];
 // device address comes from hipGetSymbolAddress, once per device, below.
 static __device__ __align__(256) float scratch[WUSH_GEMM_SCRATCH_BYTES / sizeof(float)];
 void* g_scratch[kMaxDevices];
+int g_cus[kMaxDevices];
 
 }  // namespace
 
@@ -31,6 +32,10 @@ int device_setup(int* dev) {
     if (e != hipSuccess) return (int)e;
     if (d < 0 || d >= kMaxDevices) return (int)hipErrorInvalidDevice;
     std::call_once(g_once[d], [d] {
+        int cus = 0;
+        g_cus[d] = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, d) == hipSuccess && cus > 0
+                       ? cus
+                       : 256;
         int st = gemm_h16_init_device();
         if (st == 0) st = gemv_init_device(d);
         if (st == 0) {
@@ -44,6 +49,8 @@ int device_setup(int* dev) {
     *dev = d;
     return g_status[d];
 }
+
+int device_cus(int dev) { return dev >= 0 && dev < kMaxDevices && g_cus[dev] > 0 ? g_cus[dev] : 256; }
 
 void* scratch_address(int dev) { return dev >= 0 && dev < kMaxDevices ? g_scratch[dev] : nullptr; }
 
