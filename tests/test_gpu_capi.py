@@ -645,8 +645,12 @@ def test_gemm_random_shapes_all_paths(capi):
 # The last two split K across workgroups (8 and 4 slices of 8 groups).
 # prefill plans: no K split, and (the last two) ragged M split into 4 and 2
 # slices of 32 groups
+# The last four take the 128-row tiles (64 < M <= 128, N >= 8192): one row
+# tile of 224 column tiles, K split over 2 slices, a partial column tile
+# (2 slices of 128 groups), 128 column tiles of K=256.
 H16_SHAPES = [(512, 32768, 256), (700, 30000, 512), (1030, 16400, 1024), (4096, 4096, 2048), (300, 33000, 512),
-              (600, 4096, 4096), (1030, 4096, 2048)]
+              (600, 4096, 4096), (1030, 4096, 2048),
+              (65, 57344, 2048), (100, 24576, 4096), (128, 16600, 8192), (128, 32768, 256)]
 
 
 def _sample(g, n, k):
@@ -753,11 +757,13 @@ def test_gemm_h16_preconverted_activations_agree(capi, M, N, K, wide):
     assert rel_fro(t, ref) < FRO_TOL
 
 
-def test_gemm_h16_int_exact_and_group_dots(capi):
+@pytest.mark.parametrize("M", [512, 128])
+def test_gemm_h16_int_exact_and_group_dots(capi, M):
     # unit scales and small codes: integer sums, exact in fp16; then scales 1
-    # on one group only and 0 elsewhere: y = D[:, :, g] exactly
-    g = rng(4510)
-    M, N, K = 512, 32768, 256
+    # on one group only and 0 elsewhere: y = D[:, :, g] exactly (M=128: the
+    # 128-row tiles)
+    g = rng(4510 + M)
+    N, K = 32768, 256
     xq = pack_codes(g.integers(-2, 3, (M, K)))
     wq = pack_codes(g.integers(-2, 3, (N, K)))
     xs = np.full((M, K // 32), 0x3F80, np.uint16)

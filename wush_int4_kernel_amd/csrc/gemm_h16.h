@@ -26,17 +26,18 @@ int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, co
 // first kernel (with every weight column's shift), then DMA'd into LDS by
 // launch_gemm_h16q.  The same fp16 operands as launch_gemm_h16, summed in
 // another K order within blocks of four groups: equal to fp32 rounding.
-// Needs 16-byte aligned scale tensors.
+// Needs 16-byte aligned scale tensors.  rows128: 128-row output tiles
+// (for 64 < M <= 128) instead of 256-row ones.
 size_t gemm_h16a_workspace_bytes(int64_t M, int64_t N, int64_t K, int splits);
 int launch_gemm_h16a(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                      uint16_t* y, float* partial, int M, int N, int K, int splits, int groups_per_split,
-                     void* a_ws, hipStream_t stream);
+                     void* a_ws, bool rows128, hipStream_t stream);
 
 // The GEMM stage of launch_gemm_h16a, one wavefront per SIMD (gemm_h16q.hip):
 // a16 / ea / eb as h16_prep_a_kernel leaves them; arguments checked there.
 int launch_gemm_h16q(const uint8_t* a16, const int* ea, const int* eb, const uint8_t* wq, const uint16_t* ws,
                      uint16_t* y, float* partial, int M, int N, int K, int groups_per_split, int splits,
-                     hipStream_t stream);
+                     bool rows128, hipStream_t stream);
 
 // The product for 32 < M <= 64 on weight matrices whose 224-column blocks
 // fill the GPU in one round (gemm_h16s.hip; the rule is gemm_h16s_shape_ok):

@@ -349,7 +349,7 @@ size_t gemm_h16a_workspace_bytes(int64_t M, int64_t N, int64_t K, int splits) {
 
 int launch_gemm_h16a(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,
                      uint16_t* y, float* partial, int M, int N, int K, int splits, int groups_per_split,
-                     void* a_ws, hipStream_t stream) {
+                     void* a_ws, bool rows128, hipStream_t stream) {
     const int G = K >> 5;
     if (M <= 0 || N <= 0 || K <= 0 || K % 256 != 0 || splits < 1 || groups_per_split <= 0 ||
         groups_per_split % 8 != 0 || (long long)splits * groups_per_split < G ||
@@ -366,7 +366,7 @@ int launch_gemm_h16a(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, c
         xq, xs, a16, ea, ws, eb, M, N, K, groups_per_split, mpad);
     const int e = (int)hipGetLastError();
     if (e != 0) return e;
-    return launch_gemm_h16q(a16, ea, eb, wq, ws, y, partial, M, N, K, groups_per_split, splits, stream);
+    return launch_gemm_h16q(a16, ea, eb, wq, ws, y, partial, M, N, K, groups_per_split, splits, rows128, stream);
 }
 
 int launch_gemm_h16(const uint8_t* xq, const uint16_t* xs, const uint8_t* wq, const uint16_t* ws,

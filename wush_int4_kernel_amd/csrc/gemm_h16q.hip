@@ -70,6 +70,9 @@ __device__ __forceinline__ void h16q_tile(uint32_t id, uint32_t NC, uint32_t NR,
     tn = (int)((g * kGroup + w % width) * 8 + x);
 }
 
+// RB: 32-row blocks per wavefront, 8 (256-row tiles) or 4 (128-row tiles, for
+// 64 < M <= 128: half the accumulators, the same weight conversion per stage).
+template <int RB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ ea, const int* __restrict__ eb,
                       const uint8_t* __restrict__ wq, const uint16_t* __restrict__ ws, uint16_t* __restrict__ y,
@@ -90,30 +93,35 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
     const int GR = K >> 5;
     const int K2 = K >> 1;
     const int limn = N - 1;
+    constexpr int TR = 32 * RB;                  // rows per tile
+    constexpr int NA = RB / 4;                   // activation row blocks DMA'd per wavefront
+    constexpr int kSlice = RB * 1024;            // bytes of one K16 slice of a stage's activations
     const int NC = (N + kH16Tile - 1) / kH16Tile;
-    const int NR = (M + kH16Tile - 1) / kH16Tile;
-    const int mpad = NR * kH16Tile, npad = NC * kH16Tile;
+    const int NR = (M + TR - 1) / TR;
+    // shifts and converted activations are laid out over 256-row padding
+    const int mpad = (M + kH16Tile - 1) / kH16Tile * kH16Tile, npad = NC * kH16Tile;
     const int per_slice = NC * NR;
 
     const int id = blockIdx.x;
     const int slice = id / per_slice;
     int tm, tn;
     h16q_tile((uint32_t)(id - slice * per_slice), (uint32_t)NC, (uint32_t)NR, tm, tn);
-    const int m0 = tm * kH16Tile;
+    const int m0 = tm * TR;
     const int n0 = tn * kH16Tile;
     const int gb = slice * groups_per_split;
     const int G = min(GR - gb, groups_per_split);
 
-    // activation DMA of this wavefront: row blocks 2w, 2w + 1, both K16 slices
-    const uint8_t* asrc = a16 + ((size_t)((m0 >> 5) + 2 * wave) * GR + gb) * 2048 + lane * 16;
+    // activation DMA of this wavefront: row blocks NA w .. NA w + NA - 1, both K16 slices
+    const uint8_t* asrc = a16 + ((size_t)((m0 >> 5) + NA * wave) * GR + gb) * 2048 + lane * 16;
     const size_t arb = (size_t)GR * 2048;
     auto issue_a = [&](int st, int slot) {
         const uint8_t* src = asrc + (size_t)min(st, G - 1) * 2048;   // past the slice: the last stage
-        const uint32_t dst = lds_addr(sA[slot]) + 2 * wave * 1024;
-        dma16(src, dst);
-        dma16(src + 1024, dst + kH16Slice);
-        dma16(src + arb, dst + 1024);
-        dma16(src + arb + 1024, dst + kH16Slice + 1024);
+        const uint32_t dst = lds_addr(sA[slot]) + NA * wave * 1024;
+#pragma unroll
+        for (int b = 0; b < NA; ++b) {
+            dma16(src + b * arb, dst + b * 1024);
+            dma16(src + b * arb + 1024, dst + kSlice + b * 1024);
+        }
     };
     // this lane's two weight columns (blocks 2w and 2w + 1): their scales
     const int colA = min(n0 + wave * 64 + l32, limn);
@@ -145,11 +153,11 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
         dma4(sa + o, s);
         dma4(sb + o, s + 256);
     };
-    v16f acc[8][2];
-    h8 fa[2][2][8];                              // [register set][K16 slice][row block]
+    v16f acc[RB][2];
+    h8 fa[2][2][RB];                             // [register set][K16 slice][row block]
     h8 fb[2][2][2];                              // [register set][K16 slice][column block]
     auto read_frag = [&](int slot, int P, int kk, int i) {
-        fa[P][kk][i] = frag_read(sA[slot] + kk * kH16Slice + i * 1024, lane);
+        fa[P][kk][i] = frag_read(sA[slot] + kk * kSlice + i * 1024, lane);
     };
     int eA = 0, eB = 0;
     // A weight batch in registers, read from its LDS buffer once: this
@@ -186,7 +194,8 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
     Batch R0, R1;                                // batches in LDS buffers 0 and 1
 
     // Prologue: shifts, activation stages 0-3, weight batches 0 and 1.
-    dma4(ea + (size_t)slice * mpad + m0 + wave * 64 + lane, lds_addr(sh_e + wave * 64));   // padded rows included
+    if (64 * wave < TR)                          // the tile's rows, padded rows included
+        dma4(ea + (size_t)slice * mpad + m0 + wave * 64 + lane, lds_addr(sh_e + wave * 64));
     dma4(eb + (size_t)slice * npad + n0 + wave * 64 + lane, lds_addr(sh_e + 256 + wave * 64));
     issue_a(0, 0);
     issue_a(1, 1);
@@ -205,15 +214,16 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) read_frag(0, 0, kk, i);
+        for (int i = 0; i < RB; ++i) read_frag(0, 0, kk, i);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = (v16f){0.0f};
     __builtin_amdgcn_sched_barrier(0);
 
     for (int s0 = 0; s0 < G; s0 += 2 * kH16Batch) {
-#pragma unroll
+        // fully unrolled: the batch registers and register sets are picked by j
+#pragma clang loop unroll(full)
         for (int j = 0; j < 2 * kH16Batch; ++j) {
             const int t = s0 + j;
             const int P = j & 1;
@@ -241,15 +251,15 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
+                for (int i = 0; i < RB; ++i) {
 #pragma unroll
                     for (int jb = 0; jb < 2; ++jb) {
                         acc[i][jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[P][kk][i], fb[P][kk][jb],
                                                                             acc[i][jb], 0, 0, 0);
-                        const int m = kk * 16 + i * 2 + jb;   // MFMA index in the stage
-                        if (m < 16) read_frag((j + 1) & 3, P ^ 1, m >> 3, m & 7);
-                        if (m == 16) convert_b(P ^ 1, Rc, sc, 0);
-                        if (m == 24) convert_b(P ^ 1, Rc, sc, 1);
+                        const int m = kk * 2 * RB + i * 2 + jb;   // MFMA index in the stage
+                        if (m < 2 * RB) read_frag((j + 1) & 3, P ^ 1, m / RB, m % RB);
+                        if (m == 2 * RB) convert_b(P ^ 1, Rc, sc, 0);
+                        if (m == 3 * RB) convert_b(P ^ 1, Rc, sc, 1);
                     }
                 }
             }
@@ -257,11 +267,11 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
             // a batch's reads, then per MFMA one activation fragment read over
             // the first 16; the conversion VALU spread over all
 #pragma unroll
-            for (int m = 0; m < 32; ++m) {
+            for (int m = 0; m < 4 * RB; ++m) {
                 if (m == 0 && (j == 3 || j == 7)) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);   // DS read: batch
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                if (m < 16) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read: activations
-                if (m < 16) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
+                if (m < 2 * RB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read: activations
+                if (m < 2 * RB) __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
                 else __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
             }
 #endif
@@ -272,9 +282,16 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
             // (10 weight DMAs at j = 3, 2 at j = 7)
             const int nb = (j >= 3 && j <= 5) ? 10 : (j == 7 || j <= 1) ? 2 : 0;
             __builtin_amdgcn_sched_barrier(0);
-            if (nb == 0) WUSH_WAIT_VMCNT(8);
-            else if (nb == 2) WUSH_WAIT_VMCNT(10);
-            else WUSH_WAIT_VMCNT(18);
+            if constexpr (NA == 2) {
+                if (nb == 0) WUSH_WAIT_VMCNT(8);
+                else if (nb == 2) WUSH_WAIT_VMCNT(10);
+                else WUSH_WAIT_VMCNT(18);
+            } else {
+                static_assert(NA == 1, "activation DMAs per stage: 2 * NA");
+                if (nb == 0) WUSH_WAIT_VMCNT(4);
+                else if (nb == 2) WUSH_WAIT_VMCNT(6);
+                else WUSH_WAIT_VMCNT(14);
+            }
             WUSH_LDS_BARRIER();
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -297,7 +314,7 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
         for (int jb = 0; jb < 2; ++jb) {
             const int col = n0 + wave * 64 + jb * 32 + l32;
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < RB; ++i)
 #pragma unroll
                 for (int q = 0; q < 16; ++q) {
                     const int rl = i * 32 + 8 * (q >> 2) + 4 * half + (q & 3);
@@ -317,7 +334,7 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
     const uint8_t* rbase = stg + (lane >> 3) * 128 + (lane & 7) * 16;
     const int* erow = sh_e + 4 * half;
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
+    for (int pass = 0; pass < RB / 4; ++pass) {
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
             const int i = 4 * pass + i4;
@@ -361,9 +378,15 @@ void gemm_h16q_kernel(const uint8_t* __restrict__ a16, const int* __restrict__ e
 
 int launch_gemm_h16q(const uint8_t* a16, const int* ea, const int* eb, const uint8_t* wq, const uint16_t* ws,
                      uint16_t* y, float* partial, int M, int N, int K, int groups_per_split, int splits,
-                     hipStream_t stream) {
-    const long long tiles = (long long)((N + kH16Tile - 1) / kH16Tile) * ((M + kH16Tile - 1) / kH16Tile) * splits;
-    gemm_h16q_kernel<<<dim3((unsigned)tiles), 256, 0, stream>>>(a16, ea, eb, wq, ws, y, partial, M, N, K,
+                     bool rows128, hipStream_t stream) {
+    const int tr = rows128 ? 128 : 256;
+    const long long tiles = (long long)((N + kH16Tile - 1) / kH16Tile) * ((M + tr - 1) / tr) * splits;
+    if (rows128) {
+        gemm_h16q_kernel<4><<<dim3((unsigned)tiles), 256, 0, stream>>>(a16, ea, eb, wq, ws, y, partial, M, N, K,
+                                                                        groups_per_split, splits);
+        return (int)hipGetLastError();
+    }
+    gemm_h16q_kernel<8><<<dim3((unsigned)tiles), 256, 0, stream>>>(a16, ea, eb, wq, ws, y, partial, M, N, K,
                                                                  groups_per_split, splits);
     return (int)hipGetLastError();
 }
