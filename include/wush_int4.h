@@ -142,10 +142,14 @@ int wush_gemm_s4(const uint8_t *xq, const uint16_t *xs, const uint8_t *wq, const
 /* wush_gemm_s4 that allocates nothing and takes no workspace: its split-K
  * partials (if the plan splits K) go to the library's static scratch of
  * WUSH_GEMM_SCRATCH_BYTES on the current device.  The plan is the one
- * wush_gemm_s4 chooses when given a workspace of WUSH_GEMM_SCRATCH_BYTES,
- * and the results are those of that call, bit for bit: a shape whose full
- * split of K would need more partials than the scratch holds is split into
- * fewer slices.  Nothing needs clearing
+ * wush_gemm_s4 chooses for a workspace of WUSH_GEMM_SCRATCH_BYTES that holds
+ * split-K partials only, and the results are those of such a call, bit for
+ * bit: a shape whose full split of K would need more partials than the
+ * scratch holds is split into fewer slices.  The scratch never holds
+ * converted activations, so where wush_gemm_s4 with a workspace converts them
+ * once (N >= 8192 at M >= 256 or 64 < M <= 128) this entry point runs the
+ * per-tile fp16 tiles or the int8 tiles: equal to the parity tolerance, not
+ * bit for bit.  Nothing needs clearing
  * between calls: every partial is written before it is summed.  All calls on
  * one device share its scratch, so calls that overlap on one device (on
  * different streams, or from different host threads without ordering) race.
