@@ -645,11 +645,12 @@ def test_gemm_random_shapes_all_paths(capi):
 # The last two split K across workgroups (8 and 4 slices of 8 groups).
 # prefill plans: no K split, and (the last two) ragged M split into 4 and 2
 # slices of 32 groups
-# The last four take the 128-row tiles (64 < M <= 128, N >= 8192): one row
-# tile of 224 column tiles, K split over 2 slices, a partial column tile
-# (2 slices of 128 groups), 128 column tiles of K=256.
+# (200, 40000, 1024): 256-row tiles at 128 < M < 256 (157 column tiles, the
+# last partial).  The last four take the 128-row tiles (64 < M <= 128,
+# N >= 8192): one row tile of 224 column tiles, K split over 2 slices, a
+# partial column tile (2 slices of 128 groups), 128 column tiles of K=256.
 H16_SHAPES = [(512, 32768, 256), (700, 30000, 512), (1030, 16400, 1024), (4096, 4096, 2048), (300, 33000, 512),
-              (600, 4096, 4096), (1030, 4096, 2048),
+              (600, 4096, 4096), (1030, 4096, 2048), (200, 40000, 1024),
               (65, 57344, 2048), (100, 24576, 4096), (128, 16600, 8192), (128, 32768, 256)]
 
 

@@ -697,10 +697,12 @@ static size_t plan_bytes(const Plan& p, int64_t M, int64_t N, int64_t K) {
 // fp16-MFMA 256x256 tiles (gemm_h16.hip) from this M when they make at least
 // this many tiles (K % 256 == 0).  Against the int8 tiles on MI355X: L70
 // M=256 (224 tiles) 249 vs 392 us, M=2048 K=N=4096 (128) 108 vs 128,
-// M=1024 K=N=8192 (128) 195 vs 217; below: L70 M=128 254 vs 238,
-// M=256 K=4096 N=24576 (96 tiles) 105 vs 100, M=512 K=N=8192 (64) 192 vs 138.
+// M=1024 K=N=8192 (128) 195 vs 217; L70 M=160 251 vs 434, M=192 239 vs 410,
+// M=224 239 vs 386 (half-empty row tiles); below: L70 M=128 254 vs 238 (the
+// 128-row tiles take it), M=256 K=4096 N=24576 (96 tiles) 105 vs 100, M=512
+// K=N=8192 (64) 192 vs 138.
 #ifndef WUSH_H16_MIN_M
-#define WUSH_H16_MIN_M 256
+#define WUSH_H16_MIN_M 129
 #endif
 #ifndef WUSH_H16_MIN_TILES
 #define WUSH_H16_MIN_TILES 128       // workgroups, counting K slices
