@@ -115,11 +115,14 @@ size_t wush_gemm_s4_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /* Group-scaled W4A4 GEMM, any M >= 1, K % 32 == 0: the product of
  * wush_gemv_int4, y (M, N) fp16.  On int8 MFMA with exact int32 group dots,
- * except for prefill shapes (K % 256 == 0, M >= 256, at least 64 tiles of
+ * except for prefill shapes (K % 256 == 0, M > 128, at least 64 tiles of
  * 256x256 or N >= 2048, and at least 128 workgroups counting the K slices of
- * at least 32 groups each that the workspace holds from M = 512) and for
- * 32 < M <= 64 with 49953 <= N <= 57344 and K % 1024 == 0 (16-byte aligned
- * codes and scales), which run fp16 MFMA on code*scale operands (exact after
+ * at least 32 groups each that the workspace holds from M = 512), for
+ * 64 < M <= 128 with N >= 8192 when the workspace holds the converted
+ * activations (128-row tiles, at least 128 workgroups with at most 2 K slices
+ * of at least 64 groups), and for 32 < M <= 64 with 49953 <= N <= 57344 and
+ * K % 1024 == 0 (16-byte aligned codes and scales), which run fp16 MFMA on
+ * code*scale operands (exact after
  * a power-of-two shift per row and column) accumulated in fp32 over all of K.
  * Both agree with the fp64 product to 2e-3 relative Frobenius (tested); a row
  * or column with a non-finite scale gives NaN there.
@@ -147,7 +150,7 @@ int wush_gemm_s4(const uint8_t *xq, const uint16_t *xs, const uint8_t *wq, const
  * bit: a shape whose full split of K would need more partials than the
  * scratch holds is split into fewer slices.  The scratch never holds
  * converted activations, so where wush_gemm_s4 with a workspace converts them
- * once (N >= 8192 at M >= 256 or 64 < M <= 128) this entry point runs the
+ * once (N >= 8192 at M > 64, on enough workgroups) this entry point runs the
  * per-tile fp16 tiles or the int8 tiles: equal to the parity tolerance, not
  * bit for bit.  Nothing needs clearing
  * between calls: every partial is written before it is summed.  All calls on
