@@ -646,12 +646,13 @@ def test_gemm_random_shapes_all_paths(capi):
 # prefill plans: no K split, and (the last two) ragged M split into 4 and 2
 # slices of 32 groups
 # (200, 40000, 1024): 256-row tiles at 128 < M < 256 (157 column tiles, the
-# last partial).  The last four take the 128-row tiles (64 < M <= 128,
-# N >= 8192): one row tile of 224 column tiles, K split over 2 slices, a
-# partial column tile (2 slices of 128 groups), 128 column tiles of K=256.
+# last partial).  The last five take the 128-row tiles (N >= 8192, at least
+# 192 workgroups): one row tile of 224 column tiles, K split over 2 slices,
+# a partial column tile (2 slices of 64 groups), 256 column tiles of K=256,
+# and M = 230 (too few 256-row tiles: two 128-row tiles, the second partial).
 H16_SHAPES = [(512, 32768, 256), (700, 30000, 512), (1030, 16400, 1024), (4096, 4096, 2048), (300, 33000, 512),
               (600, 4096, 4096), (1030, 4096, 2048), (200, 40000, 1024),
-              (65, 57344, 2048), (100, 24576, 4096), (128, 16600, 8192), (128, 32768, 256)]
+              (65, 57344, 2048), (100, 24576, 4096), (128, 24400, 4096), (128, 65536, 256), (230, 24600, 2048)]
 
 
 def _sample(g, n, k):
@@ -758,13 +759,13 @@ def test_gemm_h16_preconverted_activations_agree(capi, M, N, K, wide):
     assert rel_fro(t, ref) < FRO_TOL
 
 
-@pytest.mark.parametrize("M", [512, 128])
-def test_gemm_h16_int_exact_and_group_dots(capi, M):
+@pytest.mark.parametrize("M,N", [(512, 32768), (128, 65536)])
+def test_gemm_h16_int_exact_and_group_dots(capi, M, N):
     # unit scales and small codes: integer sums, exact in fp16; then scales 1
     # on one group only and 0 elsewhere: y = D[:, :, g] exactly (M=128: the
     # 128-row tiles)
     g = rng(4510 + M)
-    N, K = 32768, 256
+    K = 256
     xq = pack_codes(g.integers(-2, 3, (M, K)))
     wq = pack_codes(g.integers(-2, 3, (N, K)))
     xs = np.full((M, K // 32), 0x3F80, np.uint16)

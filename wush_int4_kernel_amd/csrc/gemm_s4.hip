@@ -744,17 +744,25 @@ static size_t plan_bytes(const Plan& p, int64_t M, int64_t N, int64_t K) {
 #ifndef WUSH_H16A_MIN_N
 #define WUSH_H16A_MIN_N 8192
 #endif
-// 64 < M <= this: the pre-converted-activation fp16 tiles with 128-row tiles
-// (gemm_h16q_kernel<4>) on weights of at least WUSH_H16A_MIN_N columns, in
-// place of the int8 tiles (0: off).
+// 64 < M <= this, where the 256-row fp16 tiles do not run: the
+// pre-converted-activation fp16 tiles with 128-row tiles (gemm_h16q_kernel<4>)
+// on weights of at least WUSH_H16A_MIN_N columns, when they make at least
+// WUSH_H16R_MIN_WGS workgroups, in place of the int8 tiles (0: off).
 // Measured on MI355X against the int8 tiles: L70 (K=8192, N=57344) M=128 154
 // vs 254 us, M=96 156 vs 248, M=72 147 vs 225, K=8192 N=28672 M=128 95 vs 134;
 // K=4096 N=24576 M=128 (2 K slices) 59.7 vs 67.9.  With 4 slices it was not
 // a steady gain (K=N=8192 M=128: 47.4 vs 49.8 on one box, 56.2 vs 52.3 on
 // another), and with slices of 32 groups (K=4096 N=8192) it took 40.2
-// against 32.0: hence at most 2 slices of at least 64 groups.
+// against 32.0: hence at most 2 slices of at least 64 groups.  Above M = 128
+// (256-row tiles too few): K=4096 N=24576 M=256 74.9 vs 111.4, M=192 73.1 vs
+// 102.8, K=4096 N=16384 M=200 (2 slices) 61.6 vs 75.4; with 128 workgroups
+// it lost (K=N=8192 M=256 83.7 vs 81.3, M=192 79.5 vs 66.2; K=4096 N=8192
+// M=256 54.8 vs 50.2), hence at least 192.
 #ifndef WUSH_H16R_MAX_M
-#define WUSH_H16R_MAX_M 128
+#define WUSH_H16R_MAX_M 256
+#endif
+#ifndef WUSH_H16R_MIN_WGS
+#define WUSH_H16R_MIN_WGS 192
 #endif
 #ifndef WUSH_H16R_MIN_SPLIT_GROUPS
 #define WUSH_H16R_MIN_SPLIT_GROUPS 64
@@ -835,23 +843,6 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
         p.groups_per_split = (int)gps;
         return p;
     }
-    if (allow_split && allow_a16 && scales16 && K % 256 == 0 && M > 64 && M <= WUSH_H16R_MAX_M &&
-        N >= WUSH_H16A_MIN_N) {
-        // 128-row fp16 tiles, K split while twice the workgroups still run
-        // in one round on 256 CUs (one workgroup per CU fits)
-        const int64_t tiles = ((M + 127) / 128) * ((N + 255) / 256);
-        int s = 1;
-        while (s < WUSH_H16R_MAX_SPLITS && tiles * 2 * s <= 256 && G0 % (16 * s) == 0 &&
-               G0 / (2 * s) >= WUSH_H16R_MIN_SPLIT_GROUPS &&
-               (size_t)(2 * s) * (size_t)M * (size_t)N * sizeof(float) <= ws_bytes_available)
-            s *= 2;
-        Plan q = p;
-        q.cfg = 5; q.tm = 128; q.tn = 256; q.sg = 1;
-        q.splits = s;
-        q.groups_per_split = (int)(G0 / s);
-        q.a16 = true;
-        if (tiles * s >= WUSH_H16_MIN_TILES && plan_bytes(q, M, N, K) <= ws_bytes_available) return q;
-    }
     if (allow_split && K % 256 == 0 && M >= WUSH_H16_MIN_M &&
         (((M + 255) / 256) * ((N + 255) / 256) >= WUSH_H16_FEW_TILES || N >= WUSH_H16_FEW_TILES_MIN_N)) {
         // fp16-MFMA tiles, with K split across workgroups (slices of a
@@ -873,6 +864,24 @@ static Plan make_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes_available
             }
             return p;
         }
+    }
+    if (allow_split && allow_a16 && scales16 && K % 256 == 0 && M > 64 && M <= WUSH_H16R_MAX_M &&
+        N >= WUSH_H16A_MIN_N) {
+        // 128-row fp16 tiles (where the 256-row ones do not run), K split
+        // while twice the workgroups still run in one round on 256 CUs (one
+        // workgroup per CU fits)
+        const int64_t tiles = ((M + 127) / 128) * ((N + 255) / 256);
+        int s = 1;
+        while (s < WUSH_H16R_MAX_SPLITS && tiles * 2 * s <= 256 && G0 % (16 * s) == 0 &&
+               G0 / (2 * s) >= WUSH_H16R_MIN_SPLIT_GROUPS &&
+               (size_t)(2 * s) * (size_t)M * (size_t)N * sizeof(float) <= ws_bytes_available)
+            s *= 2;
+        Plan q = p;
+        q.cfg = 5; q.tm = 128; q.tn = 256; q.sg = 1;
+        q.splits = s;
+        q.groups_per_split = (int)(G0 / s);
+        q.a16 = true;
+        if (tiles * s >= WUSH_H16R_MIN_WGS && plan_bytes(q, M, N, K) <= ws_bytes_available) return q;
     }
     const int64_t big_tiles = ((M + 32 * WUSH_PF_BM * 2 - 1) / (32 * WUSH_PF_BM * 2)) *
                               ((N + 32 * WUSH_PF_BN * 2 - 1) / (32 * WUSH_PF_BN * 2));
