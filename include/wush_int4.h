@@ -118,8 +118,8 @@ size_t wush_gemm_s4_workspace_bytes(int64_t M, int64_t N, int64_t K);
  * except for prefill shapes (K % 256 == 0, M > 128, at least 64 tiles of
  * 256x256 or N >= 2048, and at least 128 workgroups counting the K slices of
  * at least 32 groups each that the workspace holds from M = 512), for
- * 64 < M <= 128 with N >= 8192 when the workspace holds the converted
- * activations (128-row tiles, at least 128 workgroups with at most 2 K slices
+ * 64 < M <= 256 with N >= 8192 when the workspace holds the converted
+ * activations (128-row tiles, at least 192 workgroups with at most 2 K slices
  * of at least 64 groups), and for 32 < M <= 64 with 49953 <= N <= 57344 and
  * K % 1024 == 0 (16-byte aligned codes and scales), which run fp16 MFMA on
  * code*scale operands (exact after
