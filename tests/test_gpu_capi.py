@@ -814,7 +814,8 @@ def test_gemm_h16_group_dots_nonunit_scales(capi):
         assert np.array_equal(y, exact), gg
 
 
-def test_gemm_h16_group_scale_boundary(capi):
+@pytest.mark.parametrize("M,N", [(512, 32768), (128, 65536)])   # 256-row and 128-row tiles
+def test_gemm_h16_group_scale_boundary(capi, M, N):
     # One activation group at 2^-k of its row's largest scale (full 8-bit
     # significands; the largest sits in group 0, whose codes are 0), one weight
     # group nonzero.  The shifted largest scale lies in [2^12, 2^13), so the
@@ -823,8 +824,8 @@ def test_gemm_h16_group_scale_boundary(capi):
     # it rounds to fp16's subnormal spacing: each product term is off by at
     # most 2^-31 * sx_max * sw_max (2^-27 taken: generous), on top of the fp32
     # sum of 32 terms and the fp16 rounding of y.
-    g = rng(4516)
-    M, N, K = 512, 32768, 256
+    g = rng(4516 + M)
+    K = 256
     G = K // 32
     xq, _, wq, _ = _rand_operands(g, M, N, K)
     codes = unpack_codes(xq)
@@ -854,7 +855,8 @@ def test_gemm_h16_group_scale_boundary(capi):
             bound = (0.5 * ulp + 32 * 2.0 ** -24 * sx[:, None] * sw[None, :] * A[:, :, gg]
                      + 32 * 2.0 ** -27 * sx_max[:, None] * sw[None, :])
             assert (np.abs(y - exact) <= bound).all(), k
-            assert np.count_nonzero(y) > 0, k
+            if (np.abs(exact) >= 2.0 ** -22).any():   # some outputs well inside fp16's range
+                assert np.count_nonzero(y) > 0, k
 
 
 def _bf16_times_pow2(bits, e):
@@ -864,14 +866,14 @@ def _bf16_times_pow2(bits, e):
     return b.astype(np.uint16)
 
 
-def test_gemm_h16_scale_range(capi):
+@pytest.mark.parametrize("M,N,K", [(600, 24000, 1024), (100, 49000, 2048)])   # 256-row and 128-row tiles
+def test_gemm_h16_scale_range(capi, M, N, K):
     # Scales far outside fp16's range (activation rows near 2^+40, weight
     # columns near 2^-40, and a spread of 2^-12..2^+12 across the groups of a
     # row) so that every row and column needs its own power-of-two shift; the
     # products stay in fp16 range.  Compared with the oracle after removing
     # each row's and column's factor.
-    g = rng(4520)
-    M, N, K = 600, 24000, 1024
+    g = rng(4520 + M)
     xq, xs, wq, ws = _rand_operands(g, M, N, K)
     dr = g.integers(-3, 2, M)                    # outputs |y| < 2^11 * 2^2 stay finite in fp16
     dc = g.integers(-3, 2, N)
@@ -886,18 +888,19 @@ def test_gemm_h16_scale_range(capi):
     assert rel_fro(got, ref) < FRO_TOL, rel_fro(got, ref)
 
 
-def test_gemm_h16_nonfinite_scales(capi):
+@pytest.mark.parametrize("M,N", [(512, 32768), (120, 57344)])   # 256-row and 128-row tiles
+def test_gemm_h16_nonfinite_scales(capi, M, N):
     # a non-finite activation scale makes its row NaN, a non-finite weight
     # scale its column, as in the dequantized product; the rest is unaffected
-    g = rng(4530)
-    M, N, K = 512, 32768, 512
+    g = rng(4530 + M)
+    K = 512
     xq, xs, wq, ws = _rand_operands(g, M, N, K)
-    xs[3, 2] = 0x7F80                            # +inf
-    xs[300, 15] = 0xFFC0                         # NaN
-    ws[5, 1] = 0x7FC0                            # NaN
-    ws[20000, 9] = 0xFF80                        # -inf
+    bad_r, bad_c = [3, M - 12], [5, 20000]
+    xs[bad_r[0], 2] = 0x7F80                     # +inf
+    xs[bad_r[1], 15] = 0xFFC0                    # NaN
+    ws[bad_c[0], 1] = 0x7FC0                     # NaN
+    ws[bad_c[1], 9] = 0xFF80                     # -inf
     y = run_gemm(capi, xq, xs, wq, ws)
-    bad_r, bad_c = [3, 300], [5, 20000]
     assert np.isnan(y[bad_r]).all() and np.isnan(y[:, bad_c]).all()
     rows = np.array([r for r in _sample(g, M, 40) if r not in bad_r])
     cols = np.array([c for c in _sample(g, N, 1500) if c not in bad_c])
