@@ -772,7 +772,8 @@ static size_t plan_bytes(const Plan& p, int64_t M, int64_t N, int64_t K) {
 #endif
 // 8 < M <= 64 streaming kernel (gemm_s4_stream32_kernel).  K ways: 4
 // wavefronts per workgroup on wide weights, 8 on narrow ones (measured on
-// MI355X, M = 32: L70 (K=8192, N=57344) 66 us with 4, 83 with 8; K=N=8192
+// MI355X, M = 32: L70 (K=8192, N=57344) 66 us with 4, 83 with 8, 67 with 2 (M=24:
+// 62 vs 69, M=16: 59 vs 62 with 2); K=N=8192
 // 14.7 with 8, 17.8 with 4; K=28672 N=8192 33.4 with 8, 36.2 with 4; K=4096
 // N=24576 18.5 with 4, 23.4 with 8).  Three wavefronts per SIMD at M <= 32
 // (159-166 VGPRs), two at 32 < M <= 64.
